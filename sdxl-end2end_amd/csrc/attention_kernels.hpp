@@ -1,0 +1,58 @@
+// Internal launch interface between the C ABI (capi.cpp) and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdxl_hip {
+
+// Waves per workgroup of the fused kernel (32 query rows per wave).
+constexpr int kFusedWaves = 4;
+
+struct FusedAttentionParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const int32_t* key_mask;  // nullable [batch, k_seq]
+    void* o;
+    int64_t q_row_stride;  // elements
+    int64_t k_row_stride;
+    int64_t v_row_stride;
+    int64_t o_row_stride;
+    int32_t batch;
+    int32_t q_seq;
+    int32_t k_seq;
+    int32_t heads;
+    int32_t causal;
+    int32_t q_blocks;      // filled by the launcher
+    int32_t total_blocks;  // filled by the launcher
+    float scale_log2;      // softmax scale * log2(e)
+};
+
+// head_dim 64, fp16 or bf16 storage, 16-byte aligned rows.
+hipError_t launch_fused_attention_d64(const FusedAttentionParams& params, bool is_bf16, hipStream_t stream);
+int fused_attention_block_queries();
+
+struct OnlineAttentionParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    const int32_t* key_mask;
+    void* o;
+    int64_t q_row_stride;
+    int64_t k_row_stride;
+    int64_t v_row_stride;
+    int64_t o_row_stride;
+    int32_t batch;
+    int32_t q_seq;
+    int32_t k_seq;
+    int32_t heads;
+    int32_t head_dim;  // 1 .. 1024
+    int32_t causal;
+    float scale;
+};
+
+// dtype: 0 f16, 1 bf16, 2 f32 (sdxl_dtype values).
+hipError_t launch_online_attention(const OnlineAttentionParams& params, int dtype, hipStream_t stream);
+
+}  // namespace sdxl_hip

@@ -1,0 +1,147 @@
+"""Host-only checks of the C ABI (no GPU work): the library loads, exports every
+function include/sdxl_hip/attention.h declares, and reproduces the reference's
+backend spellings, eligibility rules and error behaviour
+(src/cuda/runtime.cpp:61-87, src/cuda/ops_kernels.cu:1912-1952)."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import sdxl_hip as sh
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sdxl_hip", "attention.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(sdxl_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_are_exported():
+    names = declared_functions()
+    assert set(names) == set(sh.EXPORTED_SYMBOLS)
+    out = subprocess.run(["nm", "-D", "--defined-only", sh.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for n in names:
+        assert n in exported, n
+    lib = sh.load()
+    for n in names:
+        assert hasattr(lib, n)
+    assert lib.sdxl_abi_version() == 1
+
+
+@pytest.mark.parametrize("name,value", [
+    ("auto", sh.AUTO), ("AUTO", sh.AUTO),
+    ("cudnn", sh.CUDNN_SDPA), ("cudnn-sdpa", sh.CUDNN_SDPA), ("sdpa", sh.CUDNN_SDPA),
+    ("flash", sh.FLASH_SM80), ("flash-sm80", sh.FLASH_SM80), ("flash2", sh.FLASH_SM80),
+    ("Flash-GFX950", sh.FLASH_SM80),
+    ("warp", sh.WARP_ONLINE), ("warp-online", sh.WARP_ONLINE), ("reference", sh.WARP_ONLINE),
+    ("wave-online", sh.WARP_ONLINE),
+])
+def test_backend_spellings(name, value):
+    assert sh.parse_backend(name) == value
+
+
+def test_unknown_backend_message():
+    with pytest.raises(sh.SdxlError) as e:
+        sh.parse_backend("triton")
+    assert e.value.status == sh.INVALID_ARGUMENT
+    assert str(e.value) == "attention backend must be auto, cudnn-sdpa, flash-sm80, or warp-online"
+
+
+def test_backend_names():
+    assert [sh.backend_name(b) for b in range(4)] == ["auto", "cudnn-sdpa", "flash-sm80", "warp-online"]
+    assert sh.backend_name(9) == "unknown"
+    lib = sh.load()
+    assert lib.sdxl_attn_kernel_name(sh.FLASH_SM80) == b"flash-gfx950"
+    assert lib.sdxl_attn_kernel_name(sh.CUDNN_SDPA) == b"flash-gfx950"
+    assert lib.sdxl_attn_kernel_name(sh.WARP_ONLINE) == b"wave-online"
+
+
+def test_auto_resolution():
+    # every SDXL UNet shape (head_dim 64, fp16) goes to the fused kernel
+    for sq, sk, h in ((4096, 4096, 10), (1024, 1024, 20), (4096, 77, 10), (1024, 77, 20), (77, 77, 20), (2, 2, 1)):
+        assert sh.resolve_backend(sh.make_desc(2, sq, sk, h)) == sh.FLASH_SM80
+    assert sh.resolve_backend(sh.make_desc(2, 64, 64, 2, dtype=sh.BF16)) == sh.FLASH_SM80
+    # D != 64 or FP32 -> wave-online (VAE head D = 512, reference vae.cpp:89-92)
+    assert sh.resolve_backend(sh.make_desc(1, 4096, 4096, 1, head_dim=512, dtype=sh.F32)) == sh.WARP_ONLINE
+    assert sh.resolve_backend(sh.make_desc(1, 8, 8, 1, head_dim=80)) == sh.WARP_ONLINE
+    # row strides that break 16-byte rows -> wave-online
+    assert sh.resolve_backend(sh.make_desc(1, 8, 8, 1, strides=(68, 0, 0, 0))) == sh.WARP_ONLINE
+    # fused QKV slices (stride 3*H*D) stay fused
+    assert sh.resolve_backend(sh.make_desc(2, 4096, 4096, 10, strides=(1920, 1920, 1920, 640))) == sh.FLASH_SM80
+
+
+def test_explicit_backend_eligibility_errors():
+    d = sh.make_desc(1, 16, 16, 1, head_dim=80, backend=sh.FLASH_SM80)
+    with pytest.raises(sh.SdxlError) as e:
+        sh.resolve_backend(d)
+    assert e.value.status == sh.UNSUPPORTED
+    d = sh.make_desc(1, 16, 16, 1, backend=sh.CUDNN_SDPA)
+    assert sh.resolve_backend(d) == sh.CUDNN_SDPA
+    with pytest.raises(sh.SdxlError) as e:
+        sh.resolve_backend(d, has_key_mask=True)  # reference: cudnn-sdpa refuses an explicit mask
+    assert e.value.status == sh.UNSUPPORTED
+    d = sh.make_desc(1, 16, 16, 1, head_dim=80, dtype=sh.F32, backend=sh.WARP_ONLINE)
+    assert sh.resolve_backend(d) == sh.WARP_ONLINE
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(heads=0), sh.INVALID_SHAPE),
+    (dict(head_dim=0), sh.INVALID_SHAPE),
+    (dict(head_dim=2048), sh.INVALID_SHAPE),
+    (dict(q_seq=-1), sh.INVALID_SHAPE),
+    (dict(strides=(32, 0, 0, 0)), sh.INVALID_SHAPE),
+    (dict(dtype=7), sh.INVALID_ARGUMENT),
+    (dict(backend=9), sh.INVALID_ARGUMENT),
+    (dict(scale=-1.0), sh.INVALID_ARGUMENT),
+])
+def test_invalid_descriptors(kw, status):
+    base = dict(batch=1, q_seq=8, k_seq=8, heads=1)
+    base.update(kw)
+    d = sh.make_desc(**base)
+    with pytest.raises(sh.SdxlError) as e:
+        sh.resolve_backend(d)
+    assert e.value.status == status
+    # sdxl_attn_fwd validates before touching the device
+    with pytest.raises(sh.SdxlError) as e:
+        sh.fwd_raw(d, 16, 16, 16, 0, 16, 0)
+    assert e.value.status == status
+
+
+def test_head_dim_message_matches_reference():
+    with pytest.raises(sh.SdxlError) as e:
+        sh.resolve_backend(sh.make_desc(1, 8, 8, 1, head_dim=1025))
+    assert str(e.value) == "CUDA attention head dimension must be in [1,1024]"
+
+
+def test_reserved_must_be_zero_and_null_pointers():
+    d = sh.make_desc(1, 8, 8, 1)
+    d.reserved = 1
+    with pytest.raises(sh.SdxlError):
+        sh.fwd_raw(d, 16, 16, 16, 0, 16, 0)
+    d = sh.make_desc(1, 8, 8, 1)
+    with pytest.raises(sh.SdxlError) as e:
+        sh.fwd_raw(d, 0, 16, 16, 0, 16, 0)
+    assert e.value.status == sh.INVALID_ARGUMENT
+
+
+def test_empty_problem_is_a_no_op():
+    # B = 0 or Sq = 0: nothing to launch, no device access at all
+    sh.fwd_raw(sh.make_desc(0, 8, 8, 1), 0, 0, 0, 0, 0, 0)
+    sh.fwd_raw(sh.make_desc(1, 0, 8, 1), 0, 0, 0, 0, 0, 0)
+
+
+def test_torch_wrapper_shape_checks():
+    torch = pytest.importorskip("torch")
+    q = torch.zeros(1, 8, 64, dtype=torch.float16)
+    k = torch.zeros(1, 8, 64, dtype=torch.float16)
+    with pytest.raises(sh.SdxlError, match="CUDA attention mismatch"):
+        sh.attention(q, k, torch.zeros(1, 9, 64, dtype=torch.float16), 1)
+    with pytest.raises(sh.SdxlError, match="CUDA attention mismatch"):
+        sh.attention(q, k, k, 3)
+    with pytest.raises(sh.SdxlError, match="key mask mismatch"):
+        sh.attention(q, k, k, 1, key_mask=torch.ones(1, 8, dtype=torch.int64))
