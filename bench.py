@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Benchmark of the SDXL UNet attention hot path on one MI355X.
+
+Headline (BASELINE.json metric): attention TFLOP/s and us/call of the level-1
+self-attention, fp16 Q,K,V [2, 10, 4096, 64] (configs[2]; BSHD storage
+[2, 4096, 640]), through the C ABI (sdxl_attn_fwd, backend auto -> flash-gfx950).
+
+One "step" = one sdxl_attn_fwd call over the whole [2, 10, 4096, 4096] problem,
+inputs resident in HBM. Timing: W untimed warm-up calls, then K calls bracketed
+by torch.cuda.synchronize(); per-launch HIP events on the launch stream give
+the kernel's average duration for the roofline figure.
+
+Also printed (same JSON line): the roofline object, the CPU baseline (the
+reference's own full_attention, compiled from its sources into
+oracle/_ref/libref_attention.so, on a bounded sample of the same workload) and
+the other configs' us/call as secondary measurements.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-secondary]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sdxl-end2end_amd"))
+
+METRIC = "attention TFLOP/s + µs/call, SDXL 4096-tok self-attn b2 h10 d64 fp16"
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_attention_c3_traffic.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c5...) and exit")
+    return ap.parse_args()
+
+
+def make_inputs(torch, B, Sq, Sk, H, seed):
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(seed)
+    W = H * 64
+    q = torch.randn(B, Sq, W, device="cuda:0", generator=g).half()
+    k = torch.randn(B, Sk, W, device="cuda:0", generator=g).half()
+    v = torch.randn(B, Sk, W, device="cuda:0", generator=g).half()
+    return q, k, v
+
+
+def time_calls(torch, sh, q, k, v, heads, steps, warmup):
+    """Returns (ms per step over the timed region, mean kernel ms from per-launch events)."""
+    out = torch.empty_like(q)
+    for _ in range(warmup):
+        sh.attention(q, k, v, heads, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        sh.attention(q, k, v, heads, out=out)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+    return wall_ms, kernel_ms, out
+
+
+def read_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 --pmc summary."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(q, k, v, heads_sample=6):
+    """The reference's single-threaded full_attention (src/unet.cpp:440-481) on batch 0,
+    heads 0..heads_sample-1, all query rows of the headline shape."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+    W = 64 * heads_sample
+    qs = np.ascontiguousarray(q[0:1, :, :W].float().cpu().numpy())
+    ks = np.ascontiguousarray(k[0:1, :, :W].float().cpu().numpy())
+    vs = np.ascontiguousarray(v[0:1, :, :W].float().cpu().numpy())
+    out = np.zeros_like(qs)
+    Sq, Sk = qs.shape[1], ks.shape[1]
+    if oracle.ref_available():
+        kind = "reference"
+        t0 = time.perf_counter()
+        rc = oracle.ref().ref_full_attention(qs, ks, vs, out, 1, Sq, Sk, heads_sample, 64)
+        dt = time.perf_counter() - t0
+        assert rc == 0
+    else:
+        kind = "port"
+        t0 = time.perf_counter()
+        out = oracle.attention_f32(qs, ks, vs, heads_sample, threads=1)
+        dt = time.perf_counter() - t0
+    flops = 4.0 * heads_sample * Sq * Sk * 64
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"batch 0, heads 0-{heads_sample - 1} of [2,10,{Sq},64] x {Sk} keys "
+                      f"({heads_sample}/20 of the workload), single thread, {dt:.2f} s",
+            "seconds": round(dt, 3)}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the attention "
+              "path has no cross-GPU exchange. Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import sdxl_hip as sh
+    sh.load()
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+
+    configs = {
+        "c1": (2, 1024, 1024, 20, "L2 self 32x32 latent"),
+        "c2": (2, 1024, 77, 20, "L2 cross 77-token context"),
+        "c3": (2, 4096, 4096, 10, "L1 self 64x64 latent"),
+        "c5_l1": (4, 3840, 3840, 10, "1536x640 L1 self"),
+        "c5_l2": (4, 960, 960, 20, "1536x640 L2 self"),
+        "c5_x1": (4, 3840, 77, 10, "1536x640 L1 cross"),
+        "c5_x2": (4, 960, 77, 20, "1536x640 L2 cross"),
+        "c2_l1x": (2, 4096, 77, 10, "L1 cross 77-token context"),
+    }
+    if args.only:
+        B, Sq, Sk, H, _ = configs[args.only]
+        q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)
+        time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
+        return
+
+    B, Sq, Sk, H, _ = configs["c3"]
+    q, k, v = make_inputs(torch, B, Sq, Sk, H, 1234)
+    desc = sh.make_desc(B, Sq, Sk, H)
+    backend = sh.load().sdxl_attn_kernel_name(sh.resolve_backend(desc)).decode()
+    torch.cuda.synchronize()
+    wall_ms, kernel_ms, _ = time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
+    flops = sh.attention_flops(B, H, Sq, Sk)
+    value = flops / (wall_ms * 1e-3) / 1e12
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "us_per_call": round(wall_ms * 1e3, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) fp16 Q/K/V resident in HBM)",
+        "config": {"workload": "SDXL level-1 self-attention, Q,K,V fp16 [2,10,4096,64] (BSHD [2,4096,640]), "
+                               "scale 1/8, non-causal", "batch": B, "heads": H, "q_seq": Sq, "k_seq": Sk,
+                   "head_dim": 64, "backend": backend},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP16_TFLOPS, 4), "traffic": read_traffic(),
+                     "kernel_us": round(kernel_ms * 1e3, 2),
+                     "algorithmic_flops_per_launch": flops,
+                     "algorithmic_bytes_per_launch": sh.attention_bytes(B, H, Sq, Sk)},
+    }
+
+    if not args.no_secondary:
+        sec = {}
+        for name, (b, sq, sk, h, label) in configs.items():
+            if name == "c3":
+                continue
+            qq, kk, vv = make_inputs(torch, b, sq, sk, h, 99)
+            w_ms, k_ms, _ = time_calls(torch, sh, qq, kk, vv, h, 100, 10)
+            fl = sh.attention_flops(b, h, sq, sk)
+            by = sh.attention_bytes(b, h, sq, sk)
+            sec[name] = {"shape": [b, h, sq, sk, 64], "what": label, "us_per_call": round(w_ms * 1e3, 2),
+                         "kernel_us": round(k_ms * 1e3, 2), "tflops": round(fl / (k_ms * 1e-3) / 1e12, 1),
+                         "mfma_frac": round(fl / (k_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
+                         "hbm_gbs": round(by / (k_ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            del qq, kk, vv
+        result["secondary"] = sec
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(q, k, v)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
