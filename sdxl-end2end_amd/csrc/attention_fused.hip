@@ -27,9 +27,12 @@
 //   first tile (P then lies in [0, 256], exact enough in fp16/bf16).
 //
 // LDS layout per stage: K[64][64] then V[64][64] elements, 128 B rows, the
-// eight 16-byte chunks of row r stored at chunk ^ rev3(r & 7). That swizzle
-// makes both the 16 B K-operand reads (8 consecutive rows, one chunk) and the
-// transposing V reads (4 rows, 2 chunks per 16-lane group) bank-conflict free.
+// eight 16-byte chunks of row r stored at chunk ^ swz(r), swz(r) =
+// rev3((r >> 1) & 7). The LDS serves 256 B (64 banks x 4 B) per cycle: a
+// 16 B K-operand read covers 16 consecutive rows in one chunk per cycle (rows
+// of equal parity must get distinct swizzles), a transposing V read covers 4
+// rows x 64 B per cycle (rows r and r+2 must fall in opposite chunk halves).
+// swz satisfies both, so neither read pattern has bank conflicts.
 // Tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging); each
 // lane picks the global chunk that lands in its swizzled LDS slot.
 #include <hip/hip_runtime.h>
@@ -60,6 +63,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.0f;              // log2 units
 
 __device__ __forceinline__ int rev3(int x) { return ((x & 1) << 2) | (x & 2) | ((x >> 2) & 1); }
+__device__ __forceinline__ int swz(int row) { return rev3((row >> 1) & 7); }
 
 template <bool IsBf16>
 __device__ __forceinline__ f32x16 mfma32(i16x8 a, i16x8 b, f32x16 c) {
@@ -103,39 +107,67 @@ __device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor
 
 __device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32, 64); }
 
-// Stages one 64-key tile of K and V into LDS. The 16 1-KiB load instructions
-// (8 for K, 8 for V) are split evenly over the workgroup's waves; instruction
-// n covers rows 8*(n%8) .. 8*(n%8)+7 of K (n < 8) or V (n >= 8). Rows past
-// k_seq are clamped to the last key: their scores are masked to -inf, so they
-// contribute exactly 0 and the clamp only keeps the loaded values finite.
+// Stages 64-key tiles of K and V into LDS. The 16 1-KiB load instructions of
+// a tile (8 for K, 8 for V) are split evenly over the workgroup's waves;
+// instruction n covers rows 8*(n%8) .. 8*(n%8)+7 of K (n < 8) or V (n >= 8),
+// lane l the row 8*(n%8) + l/8 and the global chunk (l%8) ^ swz(row), so that
+// it lands in its swizzled LDS slot. Addresses are a wave-uniform tile base
+// plus a per-lane 32-bit offset fixed for the whole loop. In a tile that runs
+// past k_seq the rows are clamped to the last key: their scores are masked to
+// -inf, so they contribute exactly 0; the clamp only keeps the values finite.
 template <int kWaves>
-__device__ __forceinline__ void stage_tile(const char* __restrict__ kbase, const char* __restrict__ vbase,
-                                           int64_t k_stride_bytes, int64_t v_stride_bytes, int key0,
-                                           int k_seq, char* lds_stage, int wave, int lane) {
-    constexpr int kPerWave = 16 / kWaves;
-    const int row_in_group = lane >> 3;
-    const int chunk_slot = lane & 7;
-#pragma unroll
-    for (int j = 0; j < kPerWave; ++j) {
-        const int n = wave * kPerWave + j;
-        const bool is_v = n >= 8;
-        const int row = 8 * (n & 7) + row_in_group;
-        int key = key0 + row;
-        key = key < k_seq ? key : k_seq - 1;
-        const int chunk = chunk_slot ^ rev3(row & 7);
-        const char* src = (is_v ? vbase + (int64_t)key * v_stride_bytes : kbase + (int64_t)key * k_stride_bytes) +
-                          chunk * 16;
-        char* dst = lds_stage + (is_v ? kTileBytes : 0) + 8 * (n & 7) * kRowBytes;
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)dst, 16, 0, 0);
-    }
-}
+struct TileLoader {
+    static constexpr int kPerWave = 16 / kWaves;
+    const char* base[kPerWave];  // K or V pointer (wave-uniform)
+    int64_t stride[kPerWave];    // row stride in bytes (wave-uniform)
+    int lds_off[kPerWave];       // byte offset inside a stage (wave-uniform)
+    uint32_t voff[kPerWave];     // per-lane offset from the tile base
 
-template <int kWaves, bool IsBf16>
-__global__ __launch_bounds__(kWaves * 64) void fused_attention_d64_kernel(FusedAttentionParams p) {
+    __device__ __forceinline__ void init(const char* kbase, const char* vbase, int64_t ks, int64_t vs, int wave,
+                                         int lane) {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int n = wave * kPerWave + j;
+            const bool is_v = n >= 8;
+            base[j] = is_v ? vbase : kbase;
+            stride[j] = is_v ? vs : ks;
+            lds_off[j] = (is_v ? kTileBytes : 0) + 8 * (n & 7) * kRowBytes;
+            const int row = 8 * (n & 7) + (lane >> 3);
+            voff[j] = (uint32_t)(row * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+        }
+    }
+
+    template <bool kClamp>
+    __device__ __forceinline__ void load(char* stage, int key0, int k_seq, int wave, int lane) const {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const char* tile_base = base[j] + (int64_t)key0 * stride[j];
+            uint32_t off = voff[j];
+            if constexpr (kClamp) {
+                const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
+                const int key = key0 + row < k_seq ? row : k_seq - 1 - key0;
+                off = (uint32_t)(key * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            }
+            __builtin_amdgcn_global_load_lds((const void*)(tile_base + off), (lds_void*)(stage + lds_off[j]), 16, 0, 0);
+        }
+    }
+
+    // Loads tile t (keys 64t ..) clamping only when the tile is partial.
+    __device__ __forceinline__ void load_tile(char* stage, int t, int k_seq, int wave, int lane) const {
+        const int key0 = t * kKeyTile;
+        if (key0 + kKeyTile <= k_seq) load<false>(stage, key0, k_seq, wave, lane);
+        else load<true>(stage, key0, k_seq, wave, lane);
+    }
+};
+
+template <int kWaves, bool IsBf16, bool kMaskAll>
+__global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(FusedAttentionParams p) {
     constexpr int kBlockQueries = kWaves * 32;
+    __shared__ __attribute__((aligned(16))) char stage0[kStageBytes];
+    __shared__ __attribute__((aligned(16))) char stage1[kStageBytes];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hf = lane >> 5;   // which half of the wave
     const int col = lane & 31;  // query column of this lane in the 32x32 tiles
 
@@ -183,25 +215,28 @@ __global__ __launch_bounds__(kWaves * 64) void fused_attention_d64_kernel(FusedA
         n_keys = n_keys < last_query + 1 ? n_keys : last_query + 1;
     }
     const int n_tiles = (n_keys + kKeyTile - 1) / kKeyTile;
-    // Tiles below full_tiles need no masking unless a key mask is given or, for
-    // causal calls, the tile reaches past this wave's first query.
-    const int full_tiles = p.key_mask != nullptr ? 0 : p.k_seq / kKeyTile;
+    // Tiles [0, n_plain) run without any masking code: they are complete and
+    // there is no key mask / causal limit (kMaskAll covers those calls).
+    const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
 
     // Per-lane LDS byte offsets.
-    // K operand: row 32g + col, chunk (2ks + hf) ^ rev3(col & 7).
-    const int k_swz = rev3(col & 7);
+    // K operand: row 32g + col, chunk (2ks + hf) ^ swz(col).
+    const int k_off = col * kRowBytes;
+    const int k_swz = swz(col);
     // V^T operand via transposing reads: inside each 16-lane group, lane
-    // r = 4j + qd supplies the address of key (4*hf + j) (+8 for the second
-    // read), dims 32dt + 16*((lane>>4)&1) + 4qd .. +3.
+    // r = 4j + qd supplies the address of key row 4*hf + j (+8 for the second
+    // read, which flips bit 0 of the swizzle), dims 32dt + 16*((lane>>4)&1) + 4qd .. +3.
     const int g16 = lane & 15;
     const int tr_j = g16 >> 2, tr_qd = g16 & 3;
     const int tr_key = 4 * hf + tr_j;
-    const int tr_swz = rev3(tr_key);
-    int v_off[2];
+    int v_off[2][2];  // [dt][second read]
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
         const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + (tr_qd >> 1);
-        v_off[dt] = kTileBytes + tr_key * kRowBytes + ((chunk ^ tr_swz) << 4) + ((tr_qd & 1) << 3);
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi)
+            v_off[dt][hi] = kTileBytes + (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) +
+                            ((tr_qd & 1) << 3);
     }
 
     f32x16 acc[2];
@@ -213,57 +248,72 @@ __global__ __launch_bounds__(kWaves * 64) void fused_attention_d64_kernel(FusedA
     float l_run = 0.0f;
     const float c = p.scale_log2;
 
-    __shared__ __attribute__((aligned(16))) char stage0[kStageBytes];
-    __shared__ __attribute__((aligned(16))) char stage1[kStageBytes];
+    TileLoader<kWaves> loader;
+    loader.init(kbase, vbase, ks_bytes, vs_bytes, wave, lane);
 
-    auto tile = [&](const char* stage, char* next, int t) {
+    auto tile = [&]<bool kMasked>(const char* stage, char* next, int t) {
         __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this lane's loads of tile t have landed
         __syncthreads();                     // ... and every other lane's; tile t-1 fully consumed
         // Key-mask word of this lane's key in tile t; issued before the prefetch so
         // that its wait does not also wait for the next tile's loads.
         int mask_word = 1;
-        if (p.key_mask != nullptr) {
+        if (kMasked && p.key_mask != nullptr) {
             const int key = t * kKeyTile + lane;
             mask_word = key < p.k_seq ? p.key_mask[(int64_t)b * p.k_seq + key] : 0;
         }
-        if (t + 1 < n_tiles)
-            stage_tile<kWaves>(kbase, vbase, ks_bytes, vs_bytes, (t + 1) * kKeyTile, p.k_seq, next, wave, lane);
+        if (t + 1 < n_tiles) loader.load_tile(next, t + 1, p.k_seq, wave, lane);
 
         // ---- S^T = K Q^T for the two 32-key groups of the tile.
+        i16x8 kop[2][4];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                kop[g][ks] = *(const lds_i16x8*)(stage + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
         f32x16 s[2];
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) s[g][i] = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int off = (32 * g + col) * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4);
-                const i16x8 kop = *(const lds_i16x8*)(stage + off);
-                s[g] = mfma32<IsBf16>(kop, qop[ks], s[g]);
-            }
+            for (int ks = 0; ks < 4; ++ks) s[g] = mfma32<IsBf16>(kop[g][ks], qop[ks], s[g]);
         }
 
-        // ---- masking (ragged tail, key mask, causal), only on tiles that need it.
+        // ---- masking (ragged tail, key mask, causal) on the tiles that need it.
         // vis bit j = key key0 + j exists and is not masked out (wave-uniform).
-        if (t >= full_tiles || (p.causal && t * kKeyTile + kKeyTile - 1 > q0)) {
+        if constexpr (kMasked) {
             const int key0 = t * kKeyTile;
             uint64_t vis = ~0ull;
             if (key0 + kKeyTile > p.k_seq) vis = (1ull << (p.k_seq - key0)) - 1ull;
             if (p.key_mask != nullptr) vis &= __builtin_amdgcn_ballot_w64(mask_word != 0);
-            const uint32_t lane_vis = (uint32_t)(vis >> (4 * hf)) ;
+            const uint32_t lane_vis = (uint32_t)(vis >> (4 * hf));
             const uint32_t lane_vis_hi = (uint32_t)(vis >> (32 + 4 * hf));
-            // causal: key key0 + kk + 4hf visible iff <= my_query
+            // causal: key key0 + 32g + kk + 4hf is visible iff <= my_query
             const int causal_lim = p.causal ? my_query - key0 - 4 * hf : 0x7FFFFFFF;
 #pragma unroll
             for (int g = 0; g < 2; ++g)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int kk = (i >> 2) * 8 + (i & 3);  // key offset within group, minus 4hf
+                    const int kk = (i >> 2) * 8 + (i & 3);
                     const uint32_t bits = g ? lane_vis_hi : lane_vis;
                     const bool ok = ((bits >> kk) & 1u) && (32 * g + kk <= causal_lim);
                     s[g][i] = ok ? s[g][i] : -__builtin_inff();
                 }
         }
+
+        // ---- V^T operands (independent of the softmax: issue early)
+        i16x8 vop[2][2][2];
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const char* base = stage + (32 * g + 16 * ss) * kRowBytes;
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+                    vop[g][ss][dt] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
 
         // ---- online softmax (per lane: one query, 32 of the tile's keys)
         float mx = fmaxf(s[0][0], s[0][1]);
@@ -305,23 +355,30 @@ __global__ __launch_bounds__(kWaves * 64) void fused_attention_d64_kernel(FusedA
                 const i16x8 pop = __builtin_bit_cast(
                     i16x8, (uint32_t __attribute__((ext_vector_type(4)))){pk[g][4 * ss], pk[g][4 * ss + 1],
                                                                            pk[g][4 * ss + 2], pk[g][4 * ss + 3]});
-                const int key_off = (32 * g + 16 * ss) * kRowBytes;
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_i16x4*)(stage + v_off[dt] + key_off));
-                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_i16x4*)(stage + v_off[dt] + key_off + 8 * kRowBytes));
-                    const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    acc[dt] = mfma32<IsBf16>(vop, pop, acc[dt]);
-                }
+                for (int dt = 0; dt < 2; ++dt) acc[dt] = mfma32<IsBf16>(vop[g][ss][dt], pop, acc[dt]);
             }
     };
 
-    if (n_tiles > 0) stage_tile<kWaves>(kbase, vbase, ks_bytes, vs_bytes, 0, p.k_seq, stage0, wave, lane);
-    for (int t = 0; t < n_tiles; t += 2) {
-        tile(stage0, stage1, t);
-        if (t + 1 < n_tiles) tile(stage1, stage0, t + 1);
+    // Tile t lives in stage (t & 1). Plain tiles first (unrolled by two so both
+    // LDS buffers are static), then the masked remainder.
+    if (n_tiles > 0) loader.load_tile(stage0, 0, p.k_seq, wave, lane);
+    int t = 0;
+    for (; t + 1 < n_plain; t += 2) {
+        tile.template operator()<false>(stage0, stage1, t);
+        tile.template operator()<false>(stage1, stage0, t + 1);
+    }
+    if (t < n_plain) {
+        tile.template operator()<false>(stage0, stage1, t);
+        ++t;
+        if (t < n_tiles) {
+            tile.template operator()<true>(stage1, stage0, t);
+            ++t;
+        }
+    }
+    for (; t < n_tiles; t += 2) {
+        tile.template operator()<true>(stage0, stage1, t);
+        if (t + 1 < n_tiles) tile.template operator()<true>(stage1, stage0, t + 1);
     }
 
     // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
@@ -352,13 +409,14 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     p.q_blocks = (p.q_seq + kBlockQueries - 1) / kBlockQueries;
     p.total_blocks = p.q_blocks * p.heads * p.batch;
     if (p.total_blocks == 0) return hipSuccess;
-    const size_t lds_bytes = 0;  // static LDS: two stages of K+V
+    const bool mask_all = p.causal || p.key_mask != nullptr;
+    const dim3 grid(p.total_blocks), block(64 * kFusedWaves);
     if (is_bf16) {
-        hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true>), dim3(p.total_blocks),
-                           dim3(64 * kFusedWaves), lds_bytes, stream, p);
+        if (mask_all) hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, false>), grid, block, 0, stream, p);
     } else {
-        hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, false>), dim3(p.total_blocks),
-                           dim3(64 * kFusedWaves), lds_bytes, stream, p);
+        if (mask_all) hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, false, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, false, false>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
 }

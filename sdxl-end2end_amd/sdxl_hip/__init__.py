@@ -11,7 +11,7 @@ import ctypes
 import os
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_ROOT, "lib", "libsdxl_attn.so")
+LIB_PATH = os.environ.get("SDXL_HIP_LIB") or os.path.join(PKG_ROOT, "lib", "libsdxl_attn.so")
 
 # sdxl_status
 OK, INVALID_ARGUMENT, INVALID_SHAPE, UNSUPPORTED, LAUNCH_FAILED, DEVICE_ERROR = range(6)
