@@ -58,9 +58,6 @@ constexpr int kHeadDim = 64;
 constexpr int kKeyTile = 64;
 constexpr int kRowBytes = kHeadDim * 2;                // 128
 constexpr int kTileBytes = kKeyTile * kRowBytes;       // 8 KiB
-constexpr int kStageBytes = 2 * kTileBytes;            // K + V
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleThreshold = 8.0f;              // log2 units
 
 __device__ __forceinline__ int rev3(int x) { return ((x & 1) << 2) | (x & 2) | ((x >> 2) & 1); }
 __device__ __forceinline__ int swz(int row) { return rev3((row >> 1) & 7); }
@@ -88,6 +85,26 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     }
 }
 
+// Multiplies eight packed fp16/bf16 values by c (round to nearest even).
+// Element-wise on a typed vector: writing dwords of a uint32 vector in a loop
+// while bit-casting its elements miscompiles with this toolchain.
+template <bool IsBf16>
+__device__ __forceinline__ i16x8 scale_operand(i16x8 x, float c) {
+    if constexpr (IsBf16) {
+        const bf16x8 v = __builtin_bit_cast(bf16x8, x);
+        bf16x8 r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = (__bf16)((float)v[i] * c);
+        return __builtin_bit_cast(i16x8, r);
+    } else {
+        const f16x8 v = __builtin_bit_cast(f16x8, x);
+        f16x8 r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] = (_Float16)((float)v[i] * c);
+        return __builtin_bit_cast(i16x8, r);
+    }
+}
+
 // Sum of the two packed values, added to acc in fp32.
 template <bool IsBf16>
 __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
@@ -108,7 +125,7 @@ __device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor
 __device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32, 64); }
 
 // Stages 64-key tiles of K and V into LDS. The 16 1-KiB load instructions of
-// a tile (8 for K, 8 for V) are split evenly over the workgroup's waves;
+// a K tile plus a V tile are split evenly over the workgroup's waves;
 // instruction n covers rows 8*(n%8) .. 8*(n%8)+7 of K (n < 8) or V (n >= 8),
 // lane l the row 8*(n%8) + l/8 and the global chunk (l%8) ^ swz(row), so that
 // it lands in its swizzled LDS slot. Addresses are a wave-uniform tile base
@@ -120,51 +137,57 @@ struct TileLoader {
     static constexpr int kPerWave = 16 / kWaves;
     const char* base[kPerWave];  // K or V pointer (wave-uniform)
     int64_t stride[kPerWave];    // row stride in bytes (wave-uniform)
-    int lds_off[kPerWave];       // byte offset inside a stage (wave-uniform)
     uint32_t voff[kPerWave];     // per-lane offset from the tile base
+
+    __device__ __forceinline__ static bool is_v(int wave, int j) { return wave * kPerWave + j >= 8; }
+    __device__ __forceinline__ static int lds_off(int wave, int j) { return 8 * ((wave * kPerWave + j) & 7) * kRowBytes; }
 
     __device__ __forceinline__ void init(const char* kbase, const char* vbase, int64_t ks, int64_t vs, int wave,
                                          int lane) {
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
-            const int n = wave * kPerWave + j;
-            const bool is_v = n >= 8;
-            base[j] = is_v ? vbase : kbase;
-            stride[j] = is_v ? vs : ks;
-            lds_off[j] = (is_v ? kTileBytes : 0) + 8 * (n & 7) * kRowBytes;
-            const int row = 8 * (n & 7) + (lane >> 3);
+            base[j] = is_v(wave, j) ? vbase : kbase;
+            stride[j] = is_v(wave, j) ? vs : ks;
+            const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
             voff[j] = (uint32_t)(row * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
         }
     }
 
-    template <bool kClamp>
-    __device__ __forceinline__ void load(char* stage, int key0, int k_seq, int wave, int lane) const {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const char* tile_base = base[j] + (int64_t)key0 * stride[j];
-            uint32_t off = voff[j];
-            if constexpr (kClamp) {
-                const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
-                const int key = key0 + row < k_seq ? row : k_seq - 1 - key0;
-                off = (uint32_t)(key * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-            }
-            __builtin_amdgcn_global_load_lds((const void*)(tile_base + off), (lds_void*)(stage + lds_off[j]), 16, 0, 0);
+    __device__ __forceinline__ void load_one(char* buf, int j, int tile, int k_seq, int wave, int lane) const {
+        const int key0 = tile * kKeyTile;
+        const char* tile_base = base[j] + (int64_t)key0 * stride[j];
+        uint32_t off = voff[j];
+        if (key0 + kKeyTile > k_seq) {  // partial tile: clamp rows (wave-uniform branch)
+            const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
+            const int key = key0 + row < k_seq ? row : k_seq - 1 - key0;
+            off = (uint32_t)(key * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
         }
+        __builtin_amdgcn_global_load_lds((const void*)(tile_base + off), (lds_void*)(buf + lds_off(wave, j)), 16, 0,
+                                         0);
     }
 
-    // Loads tile t (keys 64t ..) clamping only when the tile is partial.
-    __device__ __forceinline__ void load_tile(char* stage, int t, int k_seq, int wave, int lane) const {
-        const int key0 = t * kKeyTile;
-        if (key0 + kKeyTile <= k_seq) load<false>(stage, key0, k_seq, wave, lane);
-        else load<true>(stage, key0, k_seq, wave, lane);
+    // K tile k_tile into kbuf and V tile v_tile into vbuf; negative or
+    // out-of-range tiles are skipped.
+    __device__ __forceinline__ void load(char* kbuf, int k_tile, char* vbuf, int v_tile, int n_tiles, int k_seq,
+                                         int wave, int lane) const {
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const bool v = is_v(wave, j);
+            const int tile = v ? v_tile : k_tile;
+            if (tile >= 0 && tile < n_tiles) load_one(v ? vbuf : kbuf, j, tile, k_seq, wave, lane);
+        }
     }
 };
 
 template <int kWaves, bool IsBf16, bool kMaskAll>
-__global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(FusedAttentionParams p) {
+__global__ __launch_bounds__(kWaves * 64, 2) void fused_attention_d64_kernel(FusedAttentionParams p) {
     constexpr int kBlockQueries = kWaves * 32;
-    __shared__ __attribute__((aligned(16))) char stage0[kStageBytes];
-    __shared__ __attribute__((aligned(16))) char stage1[kStageBytes];
+    // K and V tiles are double buffered at different phases: while tile t's V
+    // and tile t+1's K are read, tile t+2's K and tile t+1's V are loaded.
+    __shared__ __attribute__((aligned(16))) char kbuf0[kTileBytes];
+    __shared__ __attribute__((aligned(16))) char kbuf1[kTileBytes];
+    __shared__ __attribute__((aligned(16))) char vbuf0[kTileBytes];
+    __shared__ __attribute__((aligned(16))) char vbuf1[kTileBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -197,12 +220,14 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     const int q0 = qblk * kBlockQueries + wave * 32;
     const int my_query = q0 + col;
 
-    // Q^T operand: lane holds dims 16*ks + 8*hf .. +7 of its query row.
+    const float c = p.scale_log2;
+    // Q^T operand, pre-scaled by scale*log2(e) so that the MFMA yields scores
+    // directly in log2 units: lane holds dims 16*ks + 8*hf .. +7 of its query.
     i16x8 qop[4];
     if (my_query < p.q_seq) {
         const i16x8* qrow = (const i16x8*)(qbase + (int64_t)my_query * p.q_row_stride * elem);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qop[ks] = qrow[2 * ks + hf];
+        for (int ks = 0; ks < 4; ++ks) qop[ks] = scale_operand<IsBf16>(qrow[2 * ks + hf], c);
     } else {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qop[ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
@@ -215,8 +240,8 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         n_keys = n_keys < last_query + 1 ? n_keys : last_query + 1;
     }
     const int n_tiles = (n_keys + kKeyTile - 1) / kKeyTile;
-    // Tiles [0, n_plain) run without any masking code: they are complete and
-    // there is no key mask / causal limit (kMaskAll covers those calls).
+    // Tiles [0, n_plain) are complete and need no mask (kMaskAll covers key-mask
+    // and causal calls, where every tile is masked).
     const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
 
     // Per-lane LDS byte offsets.
@@ -235,51 +260,100 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + (tr_qd >> 1);
 #pragma unroll
         for (int hi = 0; hi < 2; ++hi)
-            v_off[dt][hi] = kTileBytes + (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) +
-                            ((tr_qd & 1) << 3);
+            v_off[dt][hi] = (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) + ((tr_qd & 1) << 3);
     }
 
+    // Online-softmax state of this lane's query (shared by lanes l and l^32).
+    //   m_run     anchor in log2 units; scores enter exp2 as s*c - m_run, which
+    //             the QK^T MFMA produces directly by starting from neg_m = -m_run.
+    //   anchored  m_run has been set from a finite tile maximum.
+    // The anchor only moves on an exact-maximum pass: always for the first tile
+    // and for masked tiles, otherwise only when a tile's sum of probabilities
+    // exceeds 2^14 (some score rose more than ~9 above the anchor) or is not
+    // finite. Probabilities therefore stay below 2^16 in fp16/bf16; the anchor
+    // never exceeds the true running maximum, so nothing underflows that the
+    // exact algorithm would keep.
     f32x16 acc[2];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
-    float m_run = -__builtin_inff();
+    float m_run = 0.0f;
+    bool anchored = false;
     float l_run = 0.0f;
-    const float c = p.scale_log2;
+    f32x16 neg_m;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) neg_m[i] = 0.0f;
 
     TileLoader<kWaves> loader;
     loader.init(kbase, vbase, ks_bytes, vs_bytes, wave, lane);
 
-    auto tile = [&]<bool kMasked>(const char* stage, char* next, int t) {
-        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this lane's loads of tile t have landed
-        __syncthreads();                     // ... and every other lane's; tile t-1 fully consumed
-        // Key-mask word of this lane's key in tile t; issued before the prefetch so
-        // that its wait does not also wait for the next tile's loads.
-        int mask_word = 1;
-        if (kMasked && p.key_mask != nullptr) {
-            const int key = t * kKeyTile + lane;
-            mask_word = key < p.k_seq ? p.key_mask[(int64_t)b * p.k_seq + key] : 0;
-        }
-        if (t + 1 < n_tiles) loader.load_tile(next, t + 1, p.k_seq, wave, lane);
-
-        // ---- S^T = K Q^T for the two 32-key groups of the tile.
+    // S^T = K Q^T - m_run for the two 32-key groups of the K tile in kb.
+    auto scores = [&](const char* kb, f32x16 (&sc)[2]) {
         i16x8 kop[2][4];
 #pragma unroll
         for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
-                kop[g][ks] = *(const lds_i16x8*)(stage + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
-        f32x16 s[2];
+                kop[g][ks] = *(const lds_i16x8*)(kb + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
+            sc[g] = mfma32<IsBf16>(kop[g][0], qop[0], neg_m);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[g][i] = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) s[g] = mfma32<IsBf16>(kop[g][ks], qop[ks], s[g]);
+            for (int ks = 1; ks < 4; ++ks) sc[g] = mfma32<IsBf16>(kop[g][ks], qop[ks], sc[g]);
         }
+    };
 
-        // ---- masking (ragged tail, key mask, causal) on the tiles that need it.
+    // Exact-maximum pass over scores sc (relative to m_run): moves the anchor
+    // where needed, rescales O and l, leaves sc relative to the new anchor and
+    // returns the per-lane shift (for scores already computed with the old one).
+    auto exact_max = [&](f32x16 (&sc)[2]) -> float {
+        float mx = fmaxf(sc[0][0], sc[0][1]);
+#pragma unroll
+        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, sc[0][i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[1][i]);
+        mx = xhalf_max(mx);
+        // anchored rows move up only; unanchored rows take any finite maximum
+        const bool move = anchored ? mx > 0.0f : mx > -__builtin_inff();
+        const float shift = move ? mx : 0.0f;
+        const float alpha = anchored ? __builtin_amdgcn_exp2f(-shift) : 0.0f;
+        anchored = anchored || move;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+        l_run *= alpha;
+        m_run += shift;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) neg_m[i] = -m_run;
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[g][i] -= shift;
+        return shift;
+    };
+
+    f32x16 s[2];  // scores of the current tile
+
+    // One pipelined step: tile t's softmax and PV, overlapped with tile t+1's QK^T.
+    // kr: K of tile t+1, vr: V of tile t; kw/vw receive K of t+2 / V of t+1.
+    auto step = [&]<bool kMasked, bool kExact>(const char* kr, const char* vr, char* kw, char* vw, int t) {
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): K(t+1), V(t) of this lane landed
+        __syncthreads();                     // ... for every lane; step t-1 fully done with kw, vw
+        int mask_word = 1;
+        if (kMasked && p.key_mask != nullptr) {
+            const int key = t * kKeyTile + lane;
+            mask_word = key < p.k_seq ? p.key_mask[(int64_t)b * p.k_seq + key] : 0;
+        }
+        loader.load(kw, t + 2, vw, t + 1, n_tiles, p.k_seq, wave, lane);
+
+        // Next tile's scores (independent of this tile's softmax; stale data when
+        // t + 1 == n_tiles, never used then).
+        f32x16 s_next[2];
+        scores(kr, s_next);
+
+        // ---- masking (ragged tail, key mask, causal) of tile t.
         // vis bit j = key key0 + j exists and is not masked out (wave-uniform).
         if constexpr (kMasked) {
             const int key0 = t * kKeyTile;
@@ -301,51 +375,37 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
                 }
         }
 
-        // ---- V^T operands (independent of the softmax: issue early)
-        i16x8 vop[2][2][2];
+        // ---- softmax numerators P = exp2(s) and their sum
+        auto rebase_next = [&](float shift) {
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+            for (int g = 0; g < 2; ++g)
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss)
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const char* base = stage + (32 * g + 16 * ss) * kRowBytes;
-                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
-                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
-                    vop[g][ss][dt] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                }
-
-        // ---- online softmax (per lane: one query, 32 of the tile's keys)
-        float mx = fmaxf(s[0][0], s[0][1]);
-#pragma unroll
-        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, s[0][i]);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[1][i]);
-        mx = xhalf_max(mx);
-        const float m_tile = mx * c;
-        const bool need = m_tile > m_run + kRescaleThreshold;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-            const float m_new = need ? m_tile : m_run;
-            const float alpha = need ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-#pragma unroll
-            for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-            l_run *= alpha;
-            m_run = m_new;
-        }
-        const float neg_m = m_run == -__builtin_inff() ? 0.0f : -m_run;
-
+                for (int i = 0; i < 16; ++i) s_next[g][i] -= shift;
+        };
+        if constexpr (kExact || kMasked) rebase_next(exact_max(s));
         uint32_t pk[2][8];
+        float l_tile;
+        auto exponentiate = [&]() {
+            l_tile = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+            for (int g = 0; g < 2; ++g)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][2 * i], c, neg_m));
-                const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][2 * i + 1], c, neg_m));
-                pk[g][i] = pack2<IsBf16>(p0, p1);
-                l_run = sum2<IsBf16>(pk[g][i], l_run);
+                for (int i = 0; i < 8; ++i) {
+                    pk[g][i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s[g][2 * i]), __builtin_amdgcn_exp2f(s[g][2 * i + 1]));
+                    l_tile = sum2<IsBf16>(pk[g][i], l_tile);
+                }
+        };
+        exponentiate();
+        if constexpr (!kExact && !kMasked) {
+            // A score rose far above the anchor (sum > 2^14, or inf/NaN): redo this
+            // tile with an exact maximum. Rare: scores must exceed the first
+            // tile's maximum by about 9 (log2 units).
+            if (__builtin_amdgcn_ballot_w64(!(l_tile <= 16384.0f))) {
+                rebase_next(exact_max(s));
+                exponentiate();
             }
+        }
+        l_run += l_tile;
 
         // ---- O^T += V^T P^T
 #pragma unroll
@@ -355,30 +415,50 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
                 const i16x8 pop = __builtin_bit_cast(
                     i16x8, (uint32_t __attribute__((ext_vector_type(4)))){pk[g][4 * ss], pk[g][4 * ss + 1],
                                                                            pk[g][4 * ss + 2], pk[g][4 * ss + 3]});
+                const char* base = vr + (32 * g + 16 * ss) * kRowBytes;
 #pragma unroll
-                for (int dt = 0; dt < 2; ++dt) acc[dt] = mfma32<IsBf16>(vop[g][ss][dt], pop, acc[dt]);
+                for (int dt = 0; dt < 2; ++dt) {
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+                    const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    acc[dt] = mfma32<IsBf16>(vop, pop, acc[dt]);
+                }
             }
+#pragma unroll
+        for (int g = 0; g < 2; ++g) s[g] = s_next[g];
     };
 
-    // Tile t lives in stage (t & 1). Plain tiles first (unrolled by two so both
-    // LDS buffers are static), then the masked remainder.
-    if (n_tiles > 0) loader.load_tile(stage0, 0, p.k_seq, wave, lane);
-    int t = 0;
-    for (; t + 1 < n_plain; t += 2) {
-        tile.template operator()<false>(stage0, stage1, t);
-        tile.template operator()<false>(stage1, stage0, t + 1);
+    // Prologue: K(0), V(0), K(1) in flight, then tile 0's scores.
+    if (n_tiles > 0) {
+        loader.load(kbuf0, 0, vbuf0, 0, n_tiles, p.k_seq, wave, lane);
+        loader.load(kbuf1, 1, vbuf1, -1, n_tiles, p.k_seq, wave, lane);
+        __builtin_amdgcn_s_waitcnt(0x0070);
+        __syncthreads();
+        scores(kbuf0, s);
     }
-    if (t < n_plain) {
-        tile.template operator()<false>(stage0, stage1, t);
-        ++t;
-        if (t < n_tiles) {
-            tile.template operator()<true>(stage1, stage0, t);
+    // Step t reads K[(t+1)&1], V[t&1] and fills K[t&1], V[(t+1)&1]; unrolled by
+    // two so that every LDS buffer is a static object. Step 0 anchors the
+    // softmax; plain tiles follow, then the masked remainder.
+    int t = 0;
+    if (n_plain > 0) {
+        step.template operator()<false, true>(kbuf1, vbuf0, kbuf0, vbuf1, 0);
+        t = 1;
+        for (; t + 1 < n_plain; t += 2) {
+            step.template operator()<false, false>(kbuf0, vbuf1, kbuf1, vbuf0, t);
+            step.template operator()<false, false>(kbuf1, vbuf0, kbuf0, vbuf1, t + 1);
+        }
+        if (t < n_plain) {  // t odd
+            step.template operator()<false, false>(kbuf0, vbuf1, kbuf1, vbuf0, t);
             ++t;
         }
     }
+    if ((t & 1) && t < n_tiles) {
+        step.template operator()<true, true>(kbuf0, vbuf1, kbuf1, vbuf0, t);
+        ++t;
+    }
     for (; t < n_tiles; t += 2) {
-        tile.template operator()<true>(stage0, stage1, t);
-        if (t + 1 < n_tiles) tile.template operator()<true>(stage1, stage0, t + 1);
+        step.template operator()<true, true>(kbuf1, vbuf0, kbuf0, vbuf1, t);
+        if (t + 1 < n_tiles) step.template operator()<true, true>(kbuf0, vbuf1, kbuf1, vbuf0, t + 1);
     }
 
     // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
