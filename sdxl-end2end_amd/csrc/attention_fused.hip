@@ -7,34 +7,44 @@
 //
 // Work decomposition
 //   One workgroup = kWaves wave64s = kWaves*32 query rows of one (b, h).
-//   Every wave owns 32 query rows and walks all keys in tiles of 64.
-//   K and V tiles (64 keys x 64 dims, fp16/bf16) are staged in LDS, double
-//   buffered, and shared by the workgroup's waves.
+//   Every wave owns 32 query rows and walks all keys in tiles of 64 keys,
+//   each tile in two groups of 32 keys. K and V tiles (64 keys x 64 dims) are
+//   staged in LDS and shared by the workgroup's waves.
 //
-// Per wave and key tile (MFMA v_mfma_f32_32x32x16_{f16,bf16}):
-//   S^T[key][q] = K Q^T     : A = K rows from LDS (16 B per lane),
-//                             B = Q^T from registers (loaded once);
-//                             C layout puts one query per lane column, so the
-//                             row max / row sum are in-lane plus one
-//                             lane<->lane+32 exchange (v_permlane32_swap).
-//   P = exp2(S*scale*log2e - m)  in fp32, packed to fp16/bf16 (v_cvt_pk_*).
+// Per wave and 32-key group (MFMA v_mfma_f32_32x32x16_{f16,bf16}):
+//   S^T[key][q] = K Q^T - m : A = K rows from LDS (16 B per lane); B = Q^T
+//                             from registers, pre-scaled by scale*log2(e); the
+//                             accumulator starts at -m (the softmax anchor),
+//                             so the MFMA emits exp2 arguments directly. The C
+//                             layout puts one query per lane column: row sums
+//                             stay in-lane (plus one lane<->lane+32 exchange).
+//   P = exp2(S)              v_exp_f32, packed to fp16/bf16 (v_cvt_pk_*),
+//                             summed with v_dot2 on the packed values.
 //   O^T[d][q] += V^T P^T    : A = V^T built with ds_read_b64_tr_b16 straight
 //                             from the row-major V tile (no transpose pass),
-//                             B = P^T from the S^T accumulator registers
-//                             (no LDS round trip).
-//   Lazy rescaling: the running max used in exp2 only moves when a row's tile
-//   max exceeds it by more than 2^8, so O is rescaled almost never after the
-//   first tile (P then lies in [0, 256], exact enough in fp16/bf16).
+//                             B = P^T from the registers holding P.
+//   Software pipelining: the next group's QK^T MFMAs are issued before the
+//   current group's exp2 work, so the matrix cores and the VALU overlap inside
+//   each wave; only two 32-key score blocks are live.
 //
-// LDS layout per stage: K[64][64] then V[64][64] elements, 128 B rows, the
-// eight 16-byte chunks of row r stored at chunk ^ swz(r), swz(r) =
-// rev3((r >> 1) & 7). The LDS serves 256 B (64 banks x 4 B) per cycle: a
-// 16 B K-operand read covers 16 consecutive rows in one chunk per cycle (rows
-// of equal parity must get distinct swizzles), a transposing V read covers 4
-// rows x 64 B per cycle (rows r and r+2 must fall in opposite chunk halves).
-// swz satisfies both, so neither read pattern has bank conflicts.
-// Tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging); each
-// lane picks the global chunk that lands in its swizzled LDS slot.
+// Softmax anchoring: the anchor m only moves on an exact-maximum pass, which
+// runs for the first group, for masked groups, and when a group's sum of
+// probabilities exceeds 2^14 or is not finite (a score rose ~9 above the
+// anchor in log2 units). Probabilities stay below 2^16, representable in fp16
+// and bf16; the anchor never exceeds the true running maximum, so nothing
+// underflows that the exact algorithm keeps. With the reference's inputs the
+// exact pass runs once per row.
+//
+// LDS: a ring of three K tiles and two V tiles (40 KiB). While tile t is
+// consumed (K of t and t+1, V of t), K of t+2 and V of t+1 stream in, so each
+// load has a full tile of compute to land. Rows are 128 B; the eight 16-byte
+// chunks of row r sit at chunk ^ swz(r), swz(r) = rev3((r >> 1) & 7). The LDS
+// serves 256 B (64 banks x 4 B) per cycle: a 16 B K-operand read covers 16
+// consecutive rows of one chunk per cycle (rows of equal parity need distinct
+// swizzles) and a transposing V read covers 4 rows x 64 B per cycle (rows r
+// and r+2 must fall in opposite chunk halves); swz satisfies both.
+// Tiles move HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging), each
+// lane loading the global chunk that lands in its swizzled slot.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -50,14 +60,18 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
-typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr int kHeadDim = 64;
 constexpr int kKeyTile = 64;
-constexpr int kRowBytes = kHeadDim * 2;                // 128
-constexpr int kTileBytes = kKeyTile * kRowBytes;       // 8 KiB
+constexpr int kRowBytes = kHeadDim * 2;           // 128
+constexpr int kTileBytes = kKeyTile * kRowBytes;  // 8 KiB
+constexpr int kKRing = 3;
+constexpr int kVRing = 2;
+constexpr float kOverflowSum = 16384.0f;          // 2^14
 
 __device__ __forceinline__ int rev3(int x) { return ((x & 1) << 2) | (x & 2) | ((x >> 2) & 1); }
 __device__ __forceinline__ int swz(int row) { return rev3((row >> 1) & 7); }
@@ -124,70 +138,35 @@ __device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor
 
 __device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32, 64); }
 
-// Stages 64-key tiles of K and V into LDS. The 16 1-KiB load instructions of
-// a K tile plus a V tile are split evenly over the workgroup's waves;
-// instruction n covers rows 8*(n%8) .. 8*(n%8)+7 of K (n < 8) or V (n >= 8),
-// lane l the row 8*(n%8) + l/8 and the global chunk (l%8) ^ swz(row), so that
-// it lands in its swizzled LDS slot. Addresses are a wave-uniform tile base
-// plus a per-lane 32-bit offset fixed for the whole loop. In a tile that runs
-// past k_seq the rows are clamped to the last key: their scores are masked to
-// -inf, so they contribute exactly 0; the clamp only keeps the values finite.
-template <int kWaves>
-struct TileLoader {
-    static constexpr int kPerWave = 16 / kWaves;
-    const char* base[kPerWave];  // K or V pointer (wave-uniform)
-    int64_t stride[kPerWave];    // row stride in bytes (wave-uniform)
-    uint32_t voff[kPerWave];     // per-lane offset from the tile base
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_char*)p;
+}
 
-    __device__ __forceinline__ static bool is_v(int wave, int j) { return wave * kPerWave + j >= 8; }
-    __device__ __forceinline__ static int lds_off(int wave, int j) { return 8 * ((wave * kPerWave + j) & 7) * kRowBytes; }
+// One 1-KiB HBM -> LDS transfer: lane l copies 16 bytes from base + voff to
+// LDS byte lds + 16*l. Issued as inline assembly so that the compiler does
+// not treat every later LDS read as a possible alias of the transfer and
+// wait for it; the kernel waits explicitly (vmcnt + barrier) before it reads a
+// tile. M0 holds the wave-uniform LDS destination; nothing else in this
+// kernel uses M0 (the compiler treats it as reserved and emits no M0 users
+// here), so it is not listed as clobbered.
+__device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint32_t lds) {
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 4\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(base), "s"(lds)
+        : "memory");
+}
 
-    __device__ __forceinline__ void init(const char* kbase, const char* vbase, int64_t ks, int64_t vs, int wave,
-                                         int lane) {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            base[j] = is_v(wave, j) ? vbase : kbase;
-            stride[j] = is_v(wave, j) ? vs : ks;
-            const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
-            voff[j] = (uint32_t)(row * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-        }
-    }
-
-    __device__ __forceinline__ void load_one(char* buf, int j, int tile, int k_seq, int wave, int lane) const {
-        const int key0 = tile * kKeyTile;
-        const char* tile_base = base[j] + (int64_t)key0 * stride[j];
-        uint32_t off = voff[j];
-        if (key0 + kKeyTile > k_seq) {  // partial tile: clamp rows (wave-uniform branch)
-            const int row = 8 * ((wave * kPerWave + j) & 7) + (lane >> 3);
-            const int key = key0 + row < k_seq ? row : k_seq - 1 - key0;
-            off = (uint32_t)(key * stride[j]) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-        }
-        __builtin_amdgcn_global_load_lds((const void*)(tile_base + off), (lds_void*)(buf + lds_off(wave, j)), 16, 0,
-                                         0);
-    }
-
-    // K tile k_tile into kbuf and V tile v_tile into vbuf; negative or
-    // out-of-range tiles are skipped.
-    __device__ __forceinline__ void load(char* kbuf, int k_tile, char* vbuf, int v_tile, int n_tiles, int k_seq,
-                                         int wave, int lane) const {
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const bool v = is_v(wave, j);
-            const int tile = v ? v_tile : k_tile;
-            if (tile >= 0 && tile < n_tiles) load_one(v ? vbuf : kbuf, j, tile, k_seq, wave, lane);
-        }
-    }
-};
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
 
 template <int kWaves, bool IsBf16, bool kMaskAll>
-__global__ __launch_bounds__(kWaves * 64, 2) void fused_attention_d64_kernel(FusedAttentionParams p) {
+__global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(FusedAttentionParams p) {
     constexpr int kBlockQueries = kWaves * 32;
-    // K and V tiles are double buffered at different phases: while tile t's V
-    // and tile t+1's K are read, tile t+2's K and tile t+1's V are loaded.
-    __shared__ __attribute__((aligned(16))) char kbuf0[kTileBytes];
-    __shared__ __attribute__((aligned(16))) char kbuf1[kTileBytes];
-    __shared__ __attribute__((aligned(16))) char vbuf0[kTileBytes];
-    __shared__ __attribute__((aligned(16))) char vbuf1[kTileBytes];
+    constexpr int kLoadsPerWave = 16 / kWaves;  // 1-KiB transfers per wave and tile (K and V)
+    __shared__ __attribute__((aligned(16))) char kring[kKRing][kTileBytes];
+    __shared__ __attribute__((aligned(16))) char vring[kVRing][kTileBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -244,7 +223,41 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fused_attention_d64_kernel(Fus
     // and causal calls, where every tile is masked).
     const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
 
-    // Per-lane LDS byte offsets.
+    // ---- tile transfers: the 16 1-KiB transfers of a K tile plus a V tile are
+    // split over the waves; transfer n covers rows 8*(n%8) .. +7 of K (n < 8) or
+    // V (n >= 8); lane l takes row 8*(n%8) + l/8 and the global chunk
+    // (l%8) ^ swz(row), which lands in its swizzled slot.
+    uint32_t dma_off[kLoadsPerWave];
+#pragma unroll
+    for (int j = 0; j < kLoadsPerWave; ++j) {
+        const int n = wave * kLoadsPerWave + j;
+        const int row = 8 * (n & 7) + (lane >> 3);
+        const int64_t stride = n >= 8 ? vs_bytes : ks_bytes;
+        dma_off[j] = (uint32_t)(row * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+    }
+    // Issues the transfers of K tile kt and V tile vt (skipping tiles out of range).
+    auto issue = [&](int kt, int vt) {
+#pragma unroll
+        for (int j = 0; j < kLoadsPerWave; ++j) {
+            const int n = wave * kLoadsPerWave + j;
+            const bool is_v = n >= 8;
+            const int tile = is_v ? vt : kt;
+            if (tile < 0 || tile >= n_tiles) continue;
+            const int key0 = tile * kKeyTile;
+            const int64_t stride = is_v ? vs_bytes : ks_bytes;
+            const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * stride;
+            uint32_t off = dma_off[j];
+            if (key0 + kKeyTile > p.k_seq) {  // partial tile: clamp rows to the last key
+                const int row = 8 * (n & 7) + (lane >> 3);
+                const int key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
+                off = (uint32_t)(key * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            }
+            const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
+            lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
+        }
+    };
+
+    // ---- per-lane LDS byte offsets.
     // K operand: row 32g + col, chunk (2ks + hf) ^ swz(col).
     const int k_off = col * kRowBytes;
     const int k_swz = swz(col);
@@ -263,56 +276,38 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fused_attention_d64_kernel(Fus
             v_off[dt][hi] = (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) + ((tr_qd & 1) << 3);
     }
 
-    // Online-softmax state of this lane's query (shared by lanes l and l^32).
-    //   m_run     anchor in log2 units; scores enter exp2 as s*c - m_run, which
-    //             the QK^T MFMA produces directly by starting from neg_m = -m_run.
-    //   anchored  m_run has been set from a finite tile maximum.
-    // The anchor only moves on an exact-maximum pass: always for the first tile
-    // and for masked tiles, otherwise only when a tile's sum of probabilities
-    // exceeds 2^14 (some score rose more than ~9 above the anchor) or is not
-    // finite. Probabilities therefore stay below 2^16 in fp16/bf16; the anchor
-    // never exceeds the true running maximum, so nothing underflows that the
-    // exact algorithm would keep.
+    // ---- online-softmax state of this lane's query (shared by lanes l, l^32).
     f32x16 acc[2];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[dt][i] = 0.0f;
-    float m_run = 0.0f;
-    bool anchored = false;
+    float m_run = 0.0f;     // anchor, log2 units
+    bool anchored = false;  // m_run came from a finite maximum
     float l_run = 0.0f;
-    f32x16 neg_m;
+    f32x16 neg_m;           // -m_run in every entry: accumulator seed of QK^T
 #pragma unroll
     for (int i = 0; i < 16; ++i) neg_m[i] = 0.0f;
 
-    TileLoader<kWaves> loader;
-    loader.init(kbase, vbase, ks_bytes, vs_bytes, wave, lane);
-
-    // S^T = K Q^T - m_run for the two 32-key groups of the K tile in kb.
-    auto scores = [&](const char* kb, f32x16 (&sc)[2]) {
-        i16x8 kop[2][4];
+    // S^T - m for key group g (32 keys) of the K tile in kb.
+    auto qk = [&](const char* kb, int g) -> f32x16 {
+        i16x8 kop[4];
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+        for (int ks = 0; ks < 4; ++ks)
+            kop[ks] = *(const lds_i16x8*)(kb + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
+        f32x16 sc = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                kop[g][ks] = *(const lds_i16x8*)(kb + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            sc[g] = mfma32<IsBf16>(kop[g][0], qop[0], neg_m);
-#pragma unroll
-            for (int ks = 1; ks < 4; ++ks) sc[g] = mfma32<IsBf16>(kop[g][ks], qop[ks], sc[g]);
-        }
+        for (int ks = 1; ks < 4; ++ks) sc = mfma32<IsBf16>(kop[ks], qop[ks], sc);
+        return sc;
     };
 
-    // Exact-maximum pass over scores sc (relative to m_run): moves the anchor
-    // where needed, rescales O and l, leaves sc relative to the new anchor and
-    // returns the per-lane shift (for scores already computed with the old one).
-    auto exact_max = [&](f32x16 (&sc)[2]) -> float {
-        float mx = fmaxf(sc[0][0], sc[0][1]);
+    // Exact-maximum pass over group scores sc (relative to m_run): moves the
+    // anchor where needed, rescales O and l, leaves sc relative to the new
+    // anchor and returns the shift (for scores already computed with the old one).
+    auto exact_max = [&](f32x16& sc) -> float {
+        float mx = fmaxf(sc[0], sc[1]);
 #pragma unroll
-        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, sc[0][i]);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[1][i]);
+        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, sc[i]);
         mx = xhalf_max(mx);
         // anchored rows move up only; unanchored rows take any finite maximum
         const bool move = anchored ? mx > 0.0f : mx > -__builtin_inff();
@@ -328,138 +323,111 @@ __global__ __launch_bounds__(kWaves * 64, 2) void fused_attention_d64_kernel(Fus
 #pragma unroll
         for (int i = 0; i < 16; ++i) neg_m[i] = -m_run;
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sc[g][i] -= shift;
+        for (int i = 0; i < 16; ++i) sc[i] -= shift;
         return shift;
     };
 
-    f32x16 s[2];  // scores of the current tile
+    // One pipelined group step: softmax and PV of key group g of tile t (scores
+    // in s_cur), overlapped with the QK^T of the next group (from tile buffer
+    // kn, group gn) into s_next. vis: visibility bits of tile t (masked steps).
+    // kc: K tile of the current group (for the rare recomputation).
+    auto group_step = [&]<bool kMasked, bool kExact>(f32x16& s_cur, f32x16& s_next, const char* kc, const char* kn,
+                                                     int gn, const char* vb, int g, int t, uint64_t vis) {
+        s_next = qk(kn, gn);  // stale data past the last tile: computed, never used
 
-    // One pipelined step: tile t's softmax and PV, overlapped with tile t+1's QK^T.
-    // kr: K of tile t+1, vr: V of tile t; kw/vw receive K of t+2 / V of t+1.
-    auto step = [&]<bool kMasked, bool kExact>(const char* kr, const char* vr, char* kw, char* vw, int t) {
-        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): K(t+1), V(t) of this lane landed
-        __syncthreads();                     // ... for every lane; step t-1 fully done with kw, vw
-        int mask_word = 1;
-        if (kMasked && p.key_mask != nullptr) {
-            const int key = t * kKeyTile + lane;
-            mask_word = key < p.k_seq ? p.key_mask[(int64_t)b * p.k_seq + key] : 0;
-        }
-        loader.load(kw, t + 2, vw, t + 1, n_tiles, p.k_seq, wave, lane);
-
-        // Next tile's scores (independent of this tile's softmax; stale data when
-        // t + 1 == n_tiles, never used then).
-        f32x16 s_next[2];
-        scores(kr, s_next);
-
-        // ---- masking (ragged tail, key mask, causal) of tile t.
-        // vis bit j = key key0 + j exists and is not masked out (wave-uniform).
         if constexpr (kMasked) {
-            const int key0 = t * kKeyTile;
-            uint64_t vis = ~0ull;
-            if (key0 + kKeyTile > p.k_seq) vis = (1ull << (p.k_seq - key0)) - 1ull;
-            if (p.key_mask != nullptr) vis &= __builtin_amdgcn_ballot_w64(mask_word != 0);
-            const uint32_t lane_vis = (uint32_t)(vis >> (4 * hf));
-            const uint32_t lane_vis_hi = (uint32_t)(vis >> (32 + 4 * hf));
-            // causal: key key0 + 32g + kk + 4hf is visible iff <= my_query
+            const int key0 = t * kKeyTile + 32 * g;
+            const uint32_t lane_vis = (uint32_t)(vis >> (32 * g + 4 * hf));
+            // causal: key key0 + kk + 4hf is visible iff <= my_query
             const int causal_lim = p.causal ? my_query - key0 - 4 * hf : 0x7FFFFFFF;
 #pragma unroll
-            for (int g = 0; g < 2; ++g)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int kk = (i >> 2) * 8 + (i & 3);
-                    const uint32_t bits = g ? lane_vis_hi : lane_vis;
-                    const bool ok = ((bits >> kk) & 1u) && (32 * g + kk <= causal_lim);
-                    s[g][i] = ok ? s[g][i] : -__builtin_inff();
-                }
+            for (int i = 0; i < 16; ++i) {
+                const int kk = (i >> 2) * 8 + (i & 3);
+                const bool ok = ((lane_vis >> kk) & 1u) && (kk <= causal_lim);
+                s_cur[i] = ok ? s_cur[i] : -__builtin_inff();
+            }
         }
 
-        // ---- softmax numerators P = exp2(s) and their sum
         auto rebase_next = [&](float shift) {
 #pragma unroll
-            for (int g = 0; g < 2; ++g)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) s_next[g][i] -= shift;
+            for (int i = 0; i < 16; ++i) s_next[i] -= shift;
         };
-        if constexpr (kExact || kMasked) rebase_next(exact_max(s));
-        uint32_t pk[2][8];
-        float l_tile;
+        if constexpr (kExact || kMasked) rebase_next(exact_max(s_cur));
+        uint32_t pk[8];
+        float l_grp;
         auto exponentiate = [&]() {
-            l_tile = 0.0f;
+            l_grp = 0.0f;
 #pragma unroll
-            for (int g = 0; g < 2; ++g)
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    pk[g][i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s[g][2 * i]), __builtin_amdgcn_exp2f(s[g][2 * i + 1]));
-                    l_tile = sum2<IsBf16>(pk[g][i], l_tile);
-                }
+            for (int i = 0; i < 8; ++i) {
+                pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
+                l_grp = sum2<IsBf16>(pk[i], l_grp);
+            }
         };
         exponentiate();
         if constexpr (!kExact && !kMasked) {
-            // A score rose far above the anchor (sum > 2^14, or inf/NaN): redo this
-            // tile with an exact maximum. Rare: scores must exceed the first
-            // tile's maximum by about 9 (log2 units).
-            if (__builtin_amdgcn_ballot_w64(!(l_tile <= 16384.0f))) {
-                rebase_next(exact_max(s));
+            if (__builtin_amdgcn_ballot_w64(!(l_grp <= kOverflowSum))) {
+                // Recompute this group's scores (its K tile is still resident)
+                // rather than keep them live across the exponentials; the
+                // memory clobber forces the operands to be re-read.
+                asm volatile("" ::: "memory");
+                s_cur = qk(kc, g);
+                rebase_next(exact_max(s_cur));
                 exponentiate();
             }
         }
-        l_run += l_tile;
+        l_run += l_grp;
 
-        // ---- O^T += V^T P^T
+        // O^T += V^T P^T over the group's two 16-key MFMA steps.
 #pragma unroll
-        for (int g = 0; g < 2; ++g)
+        for (int ss = 0; ss < 2; ++ss) {
+            const i16x8 pop = __builtin_bit_cast(i16x8, u32x4{pk[4 * ss], pk[4 * ss + 1], pk[4 * ss + 2], pk[4 * ss + 3]});
+            const char* base = vb + (32 * g + 16 * ss) * kRowBytes;
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
-                const i16x8 pop = __builtin_bit_cast(
-                    i16x8, (uint32_t __attribute__((ext_vector_type(4)))){pk[g][4 * ss], pk[g][4 * ss + 1],
-                                                                           pk[g][4 * ss + 2], pk[g][4 * ss + 3]});
-                const char* base = vr + (32 * g + 16 * ss) * kRowBytes;
-#pragma unroll
-                for (int dt = 0; dt < 2; ++dt) {
-                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
-                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
-                    const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    acc[dt] = mfma32<IsBf16>(vop, pop, acc[dt]);
-                }
+            for (int dt = 0; dt < 2; ++dt) {
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+                const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                acc[dt] = mfma32<IsBf16>(vop, pop, acc[dt]);
             }
-#pragma unroll
-        for (int g = 0; g < 2; ++g) s[g] = s_next[g];
+        }
     };
 
-    // Prologue: K(0), V(0), K(1) in flight, then tile 0's scores.
+    // ---- main loop. Before tile t: K(t), K(t+1) and V(t) resident; tile t
+    // starts K(t+2) and V(t+1). sa/sb hold the scores of group 0 / group 1.
+    f32x16 sa, sb;
     if (n_tiles > 0) {
-        loader.load(kbuf0, 0, vbuf0, 0, n_tiles, p.k_seq, wave, lane);
-        loader.load(kbuf1, 1, vbuf1, -1, n_tiles, p.k_seq, wave, lane);
-        __builtin_amdgcn_s_waitcnt(0x0070);
+        issue(0, 0);
+        issue(1, -1);
+        wait_vmem_all();
         __syncthreads();
-        scores(kbuf0, s);
+        sa = qk(kring[0], 0);
     }
-    // Step t reads K[(t+1)&1], V[t&1] and fills K[t&1], V[(t+1)&1]; unrolled by
-    // two so that every LDS buffer is a static object. Step 0 anchors the
-    // softmax; plain tiles follow, then the masked remainder.
+    auto tile = [&]<bool kMasked, bool kFirst>(int t) {
+        wait_vmem_all();
+        __syncthreads();
+        uint64_t vis = ~0ull;
+        if constexpr (kMasked) {
+            const int key0 = t * kKeyTile;
+            if (p.key_mask != nullptr) {
+                const int key = key0 + lane;
+                const int word = key < p.k_seq ? p.key_mask[(int64_t)b * p.k_seq + key] : 0;
+                vis = __builtin_amdgcn_ballot_w64(word != 0);
+            }
+            if (key0 + kKeyTile > p.k_seq) vis &= (1ull << (p.k_seq - key0)) - 1ull;
+        }
+        issue(t + 2, t + 1);
+        const char* k_t = kring[t % kKRing];
+        const char* k_t1 = kring[(t + 1) % kKRing];
+        const char* v_t = vring[t % kVRing];
+        group_step.template operator()<kMasked, kMasked || kFirst>(sa, sb, k_t, k_t, 1, v_t, 0, t, vis);
+        group_step.template operator()<kMasked, kMasked>(sb, sa, k_t, k_t1, 0, v_t, 1, t, vis);
+    };
     int t = 0;
     if (n_plain > 0) {
-        step.template operator()<false, true>(kbuf1, vbuf0, kbuf0, vbuf1, 0);
-        t = 1;
-        for (; t + 1 < n_plain; t += 2) {
-            step.template operator()<false, false>(kbuf0, vbuf1, kbuf1, vbuf0, t);
-            step.template operator()<false, false>(kbuf1, vbuf0, kbuf0, vbuf1, t + 1);
-        }
-        if (t < n_plain) {  // t odd
-            step.template operator()<false, false>(kbuf0, vbuf1, kbuf1, vbuf0, t);
-            ++t;
-        }
+        tile.template operator()<false, true>(0);
+        for (t = 1; t < n_plain; ++t) tile.template operator()<false, false>(t);
     }
-    if ((t & 1) && t < n_tiles) {
-        step.template operator()<true, true>(kbuf0, vbuf1, kbuf1, vbuf0, t);
-        ++t;
-    }
-    for (; t < n_tiles; t += 2) {
-        step.template operator()<true, true>(kbuf1, vbuf0, kbuf0, vbuf1, t);
-        if (t + 1 < n_tiles) step.template operator()<true, true>(kbuf0, vbuf1, kbuf1, vbuf0, t + 1);
-    }
+    for (; t < n_tiles; ++t) tile.template operator()<true, false>(t);
 
     // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
     // dims 32dt + 8u + 4hf + (0..3) of its query in acc[dt][4u .. 4u+3].
