@@ -40,6 +40,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c5...) and exit")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
 
 
@@ -138,6 +140,14 @@ def main():
         "c5_x2": (4, 960, 77, 20, "1536x640 L2 cross"),
         "c2_l1x": (2, 4096, 77, 10, "L1 cross 77-token context"),
     }
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)

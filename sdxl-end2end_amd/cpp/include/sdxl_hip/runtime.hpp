@@ -1,0 +1,78 @@
+// Runtime, error and backend-selection types of the sdxl_hip C++20 host API.
+//
+// Mirrors the reference's include/sdxl/cuda/runtime.hpp (AttentionBackend at
+// :53-58, parse/name at :60-61, RuntimeOptions::attention_backend at :96,
+// Runtime at :127-161) for the attention path: one device, one stream per
+// Runtime, exceptions for every failure.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <string_view>
+#include <vector>
+
+namespace sdxl::hip {
+
+// Thrown for every failure (reference CudaError, runtime.hpp:18-21).
+class HipError final : public std::runtime_error {
+public:
+    explicit HipError(const std::string& message) : std::runtime_error(message) {}
+};
+
+void check_hip(hipError_t status, std::string_view expression, std::string_view file, int line);
+#define SDXL_HIP_CHECK(expr) ::sdxl::hip::check_hip((expr), #expr, __FILE__, __LINE__)
+
+// Same enumerators and spellings as the reference. On MI355X CuDnnSDPA and
+// FlashSM80 both run the fused gfx950 kernel (flash-gfx950); WarpOnline runs
+// the wave64 online-softmax kernel; Auto picks the fused kernel whenever it is
+// eligible (head_dim 64, fp16/bf16), else WarpOnline.
+enum class AttentionBackend : std::uint8_t { Auto, CuDnnSDPA, FlashSM80, WarpOnline };
+
+[[nodiscard]] AttentionBackend parse_attention_backend(std::string_view value);
+[[nodiscard]] const char* attention_backend_name(AttentionBackend backend) noexcept;
+
+struct RuntimeOptions {
+    int device = 0;
+    AttentionBackend attention_backend = AttentionBackend::Auto;
+    // Record an event pair around every Ops call (reference ProfileScope,
+    // include/sdxl/cuda/profiler.hpp:32-53); read with Runtime::profile_records().
+    bool profile = false;
+};
+
+struct ProfileRecord {
+    std::string label;
+    float milliseconds = 0.0F;
+};
+
+struct RuntimeState;
+
+class Runtime final {
+public:
+    explicit Runtime(RuntimeOptions options = {});
+    ~Runtime();
+    Runtime(const Runtime&) = delete;
+    Runtime& operator=(const Runtime&) = delete;
+    Runtime(Runtime&&) noexcept = default;
+    Runtime& operator=(Runtime&&) noexcept = default;
+
+    [[nodiscard]] hipStream_t stream() const noexcept;
+    [[nodiscard]] int device() const noexcept;
+    [[nodiscard]] const RuntimeOptions& options() const noexcept;
+    void synchronize() const;
+
+    // Opens an event-pair scope on the runtime stream; returns an id for end_profile.
+    // No-op (returns -1) unless RuntimeOptions::profile is set. Never synchronises.
+    [[nodiscard]] int begin_profile(std::string label) const;
+    void end_profile(int id) const;
+    // Synchronises and resolves every recorded scope, in order.
+    [[nodiscard]] std::vector<ProfileRecord> profile_records() const;
+
+private:
+    std::unique_ptr<RuntimeState> state_;
+};
+
+}  // namespace sdxl::hip

@@ -1,0 +1,88 @@
+"""Summaries of rocprofv3 output for the attention kernels (CSV output format).
+
+  python -m sdxl_hip.profiling stats <dir>            kernel-trace stats (per-kernel avg duration)
+  python -m sdxl_hip.profiling counters <dir> [name]  mean PMC counter value per dispatch of a kernel
+  python -m sdxl_hip.profiling traffic --kernel NAME --fetch DIR --write DIR
+                                       --copy-fetch DIR --copy-write DIR --copy-mib N
+      HBM bytes per launch of NAME from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled
+      by what the same counter reads for a device copy of N MiB (read N MiB, write N MiB).
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+from collections import defaultdict
+
+
+def _rows(root: str, suffix: str):
+    for f in sorted(glob.glob(os.path.join(root, "**", f"*{suffix}"), recursive=True)):
+        with open(f) as fh:
+            yield from csv.DictReader(fh)
+
+
+def kernel_stats(root: str):
+    """{kernel: (calls, avg_ns, total_ns)} from *kernel_stats.csv (or *kernel_trace.csv)."""
+    out = {}
+    for r in _rows(root, "kernel_stats.csv"):
+        out[r["Name"]] = (int(r["Calls"]), float(r["AverageNs"]), float(r["TotalDurationNs"]))
+    if not out:
+        acc = defaultdict(list)
+        for r in _rows(root, "kernel_trace.csv"):
+            acc[r["Kernel_Name"]].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        out = {k: (len(v), sum(v) / len(v), float(sum(v))) for k, v in acc.items()}
+    return out
+
+
+def counters(root: str, kernel_substr: str = ""):
+    """{counter: mean value per dispatch} over dispatches whose kernel name contains kernel_substr.
+    Values of one dispatch are summed over instances first (rocprofv3 may emit one row per XCD)."""
+    per_dispatch = defaultdict(lambda: defaultdict(float))
+    for r in _rows(root, "counter_collection.csv"):
+        if kernel_substr and kernel_substr not in r.get("Kernel_Name", ""):
+            continue
+        per_dispatch[r["Counter_Name"]][r.get("Dispatch_Id", "0")] += float(r["Counter_Value"])
+    return {k: sum(v.values()) / len(v) for k, v in per_dispatch.items() if v}
+
+
+def traffic(kernel: str, fetch_dir: str, write_dir: str, copy_fetch: str, copy_write: str, copy_mib: float):
+    copy_bytes = copy_mib * (1 << 20)
+    f_k = counters(fetch_dir, kernel)["FETCH_SIZE"] * 1024.0
+    w_k = counters(write_dir, kernel)["WRITE_SIZE"] * 1024.0
+    f_c = counters(copy_fetch, "")["FETCH_SIZE"] * 1024.0
+    w_c = counters(copy_write, "")["WRITE_SIZE"] * 1024.0
+    f_scale = copy_bytes / f_c
+    w_scale = copy_bytes / w_c
+    return {"fetch_bytes_raw": f_k, "write_bytes_raw": w_k, "fetch_scale": f_scale, "write_scale": w_scale,
+            "fetch_bytes": f_k * f_scale, "write_bytes": w_k * w_scale,
+            "traffic_bytes": f_k * f_scale + w_k * w_scale}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    a = sub.add_parser("stats")
+    a.add_argument("dir")
+    b = sub.add_parser("counters")
+    b.add_argument("dir")
+    b.add_argument("name", nargs="?", default="")
+    c = sub.add_parser("traffic")
+    for k in ("kernel", "fetch", "write", "copy_fetch", "copy_write"):
+        c.add_argument("--" + k.replace("_", "-"), required=True)
+    c.add_argument("--copy-mib", type=float, required=True)
+    args = ap.parse_args()
+    if args.cmd == "stats":
+        for name, (calls, avg, tot) in sorted(kernel_stats(args.dir).items(), key=lambda x: -x[1][2]):
+            print(f"{avg / 1e3:10.2f} us avg  {calls:6d} calls  {tot / 1e6:9.3f} ms total  {name[:110]}")
+    elif args.cmd == "counters":
+        for k, v in sorted(counters(args.dir, args.name).items()):
+            print(f"{k:32s} {v:18.1f}")
+    else:
+        t = traffic(args.kernel, args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_mib)
+        for k, v in t.items():
+            print(f"{k}: {v:.6g}")
+
+
+if __name__ == "__main__":
+    main()
