@@ -35,9 +35,9 @@
 // underflows that the exact algorithm keeps. With the reference's inputs the
 // exact pass runs once per row.
 //
-// LDS: a ring of three K tiles and two V tiles (40 KiB). While tile t is
-// consumed (K of t and t+1, V of t), K of t+2 and V of t+1 stream in, so each
-// load has a full tile of compute to land. Rows are 128 B; the eight 16-byte
+// LDS: two K tiles and two V tiles (32 KiB). While tile t is consumed (its V,
+// and K of t+1 for the next groups' operands), K of t+2 and V of t+1 stream
+// in, so each load has a full tile of compute to land. Rows are 128 B; the eight 16-byte
 // chunks of row r sit at chunk ^ swz(r), swz(r) = rev3((r >> 1) & 7). The LDS
 // serves 256 B (64 banks x 4 B) per cycle: a 16 B K-operand read covers 16
 // consecutive rows of one chunk per cycle (rows of equal parity need distinct
@@ -69,7 +69,7 @@ constexpr int kHeadDim = 64;
 constexpr int kKeyTile = 64;
 constexpr int kRowBytes = kHeadDim * 2;           // 128
 constexpr int kTileBytes = kKeyTile * kRowBytes;  // 8 KiB
-constexpr int kKRing = 3;
+constexpr int kKRing = 2;
 constexpr int kVRing = 2;
 constexpr float kOverflowSum = 16384.0f;          // 2^14
 
@@ -143,20 +143,29 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 // One 1-KiB HBM -> LDS transfer: lane l copies 16 bytes from base + voff to
-// LDS byte lds + 16*l. Issued as inline assembly so that the compiler does
-// not treat every later LDS read as a possible alias of the transfer and
-// wait for it; the kernel waits explicitly (vmcnt + barrier) before it reads a
-// tile. M0 holds the wave-uniform LDS destination; nothing else in this
-// kernel uses M0 (the compiler treats it as reserved and emits no M0 users
-// here), so it is not listed as clobbered.
+// LDS byte lds + 16*l. Issued as inline assembly so that the compiler neither
+// treats later LDS reads as possible aliases of the transfer nor waits for
+// earlier transfers before issuing the next (which a memory clobber causes).
+// Ordering is explicit instead: the volatile statement stays in program order
+// with the s_waitcnt and s_barrier builtins around it, a transfer never
+// targets a buffer read in the same tile, and every tile begins with
+// vmcnt(0) + barrier before its buffers are read. M0 holds the wave-uniform
+// LDS destination; nothing else in this kernel uses M0 (the compiler treats it
+// as reserved and emits no M0 users here), so it is not listed as clobbered.
 __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint32_t lds) {
+    // base and lds are wave-uniform by construction; readfirstlane makes that
+    // explicit so that they are allocated to SGPRs as the instruction requires.
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t ub = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    base = (const char*)(uintptr_t)ub;
+    lds = __builtin_amdgcn_readfirstlane(lds);
     asm volatile(
         "s_mov_b32 m0, %2\n\t"
         "s_nop 4\n\t"
         "global_load_lds_dwordx4 %0, %1"
         :
-        : "v"(voff), "s"(base), "s"(lds)
-        : "memory");
+        : "v"(voff), "s"(base), "s"(lds));
 }
 
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
@@ -227,16 +236,10 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     // split over the waves; transfer n covers rows 8*(n%8) .. +7 of K (n < 8) or
     // V (n >= 8); lane l takes row 8*(n%8) + l/8 and the global chunk
     // (l%8) ^ swz(row), which lands in its swizzled slot.
-    uint32_t dma_off[kLoadsPerWave];
-#pragma unroll
-    for (int j = 0; j < kLoadsPerWave; ++j) {
-        const int n = wave * kLoadsPerWave + j;
-        const int row = 8 * (n & 7) + (lane >> 3);
-        const int64_t stride = n >= 8 ? vs_bytes : ks_bytes;
-        dma_off[j] = (uint32_t)(row * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-    }
     // Issues the transfers of K tile kt and V tile vt (skipping tiles out of range).
-    auto issue = [&](int kt, int vt) {
+    // Per-lane offsets are recomputed per tile (a few ALU ops) rather than held
+    // in registers for the whole loop.
+    auto issue = [&](int kt, int vt) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kLoadsPerWave; ++j) {
             const int n = wave * kLoadsPerWave + j;
@@ -246,12 +249,10 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             const int key0 = tile * kKeyTile;
             const int64_t stride = is_v ? vs_bytes : ks_bytes;
             const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * stride;
-            uint32_t off = dma_off[j];
-            if (key0 + kKeyTile > p.k_seq) {  // partial tile: clamp rows to the last key
-                const int row = 8 * (n & 7) + (lane >> 3);
-                const int key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
-                off = (uint32_t)(key * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-            }
+            const int row = 8 * (n & 7) + (lane >> 3);
+            // partial tile: clamp rows to the last key
+            const int key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
+            const uint32_t off = (uint32_t)(key * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
             const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
             lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
         }
@@ -289,27 +290,33 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
 #pragma unroll
     for (int i = 0; i < 16; ++i) neg_m[i] = 0.0f;
 
-    // S^T - m for key group g (32 keys) of the K tile in kb.
-    auto qk = [&](const char* kb, int g) -> f32x16 {
-        i16x8 kop[4];
+    // K operands (4 x 16 B) of key group g of the K tile in kb.
+    auto load_k = [&](const char* kb, int g, i16x8 (&kop)[4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
             kop[ks] = *(const lds_i16x8*)(kb + k_off + 32 * g * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
-        f32x16 sc = mfma32<IsBf16>(kop[0], qop[0], neg_m);
+    };
+    // V^T operands of 16-key half ss of key group g of the V tile in vb: [dt].
+    auto load_v = [&](const char* vb, int g, int ss, i16x8 (&vop)[2]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ks = 1; ks < 4; ++ks) sc = mfma32<IsBf16>(kop[ks], qop[ks], sc);
-        return sc;
+        for (int dt = 0; dt < 2; ++dt) {
+            const char* base = vb + (32 * g + 16 * ss) * kRowBytes;
+            const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+            const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+            vop[dt] = i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
     };
 
-    // Exact-maximum pass over group scores sc (relative to m_run): moves the
-    // anchor where needed, rescales O and l, leaves sc relative to the new
-    // anchor and returns the shift (for scores already computed with the old one).
-    auto exact_max = [&](f32x16& sc) -> float {
-        float mx = fmaxf(sc[0], sc[1]);
+    // Exact-maximum pass over scores sc[i0, i1) (relative to m_run): moves the
+    // anchor where needed (anchored rows move up only, unanchored rows take any
+    // finite maximum), rescales O and l and returns the shift every score
+    // computed against the old anchor must subtract.
+    auto exact_max = [&](const f32x16& sc, int i0, int i1) __attribute__((always_inline)) -> float {
+        float mx = -__builtin_inff();
 #pragma unroll
-        for (int i = 2; i < 16; ++i) mx = fmaxf(mx, sc[i]);
+        for (int i = 0; i < 16; ++i)
+            if (i >= i0 && i < i1) mx = fmaxf(mx, sc[i]);
         mx = xhalf_max(mx);
-        // anchored rows move up only; unanchored rows take any finite maximum
         const bool move = anchored ? mx > 0.0f : mx > -__builtin_inff();
         const float shift = move ? mx : 0.0f;
         const float alpha = anchored ? __builtin_amdgcn_exp2f(-shift) : 0.0f;
@@ -322,19 +329,25 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         m_run += shift;
 #pragma unroll
         for (int i = 0; i < 16; ++i) neg_m[i] = -m_run;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) sc[i] -= shift;
         return shift;
     };
 
-    // One pipelined group step: softmax and PV of key group g of tile t (scores
-    // in s_cur), overlapped with the QK^T of the next group (from tile buffer
-    // kn, group gn) into s_next. vis: visibility bits of tile t (masked steps).
-    // kc: K tile of the current group (for the rare recomputation).
-    auto group_step = [&]<bool kMasked, bool kExact>(f32x16& s_cur, f32x16& s_next, const char* kc, const char* kn,
-                                                     int gn, const char* vb, int g, int t, uint64_t vis) {
-        s_next = qk(kn, gn);  // stale data past the last tile: computed, never used
-
+    // One pipelined group step (32 keys of tile t, group g; scores in s_cur).
+    // Overlapped inside the wave: the next group's QK^T chain (K operands in
+    // kop, prefetched one step earlier) runs on the matrix core while this
+    // group's exponentials run on the VALU; P.V of each 16-key half follows as
+    // soon as its probabilities are packed. The instruction order is pinned
+    // with scheduling barriers so that every dependent MFMA has independent
+    // VALU work issued between it and its predecessor (in-order issue would
+    // otherwise stall the wave on the chain). At the end, the K operands of
+    // the group after next (tile buffer kn2, group g2) are prefetched into kop.
+    // kMasked/kExact: exact maximum over the whole group first (masked tiles,
+    // first tile); otherwise each half is checked for overflow after the fact.
+    auto group_step = [&]<bool kMasked, bool kExact>(f32x16& s_cur, f32x16& s_next, i16x8 (&kop)[4], const char* vb,
+                                                     int g, int t, uint64_t vis, const char* kn2, int g2,
+                                                     bool have_next) __attribute__((always_inline)) {
+        i16x8 vop[2];
+        load_v(vb, g, 0, vop);
         if constexpr (kMasked) {
             const int key0 = t * kKeyTile + 32 * g;
             const uint32_t lane_vis = (uint32_t)(vis >> (32 * g + 4 * hf));
@@ -347,66 +360,116 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
                 s_cur[i] = ok ? s_cur[i] : -__builtin_inff();
             }
         }
-
-        auto rebase_next = [&](float shift) {
+        if constexpr (kMasked || kExact) {
+            const float shift = exact_max(s_cur, 0, 16);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s_next[i] -= shift;
-        };
-        if constexpr (kExact || kMasked) rebase_next(exact_max(s_cur));
+            for (int i = 0; i < 16; ++i) s_cur[i] -= shift;
+        }
+        float e[16];
         uint32_t pk[8];
-        float l_grp;
-        auto exponentiate = [&]() {
-            l_grp = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
-                l_grp = sum2<IsBf16>(pk[i], l_grp);
-            }
-        };
-        exponentiate();
-        if constexpr (!kExact && !kMasked) {
-            if (__builtin_amdgcn_ballot_w64(!(l_grp <= kOverflowSum))) {
-                // Recompute this group's scores (its K tile is still resident)
-                // rather than keep them live across the exponentials; the
-                // memory clobber forces the operands to be re-read.
-                asm volatile("" ::: "memory");
-                s_cur = qk(kc, g);
-                rebase_next(exact_max(s_cur));
-                exponentiate();
-            }
-        }
-        l_run += l_grp;
 
-        // O^T += V^T P^T over the group's two 16-key MFMA steps.
+        // ---- block A: QK1, QK2 with exponentials of half 0
+        s_next = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
-        for (int ss = 0; ss < 2; ++ss) {
-            const i16x8 pop = __builtin_bit_cast(i16x8, u32x4{pk[4 * ss], pk[4 * ss + 1], pk[4 * ss + 2], pk[4 * ss + 3]});
-            const char* base = vb + (32 * g + 16 * ss) * kRowBytes;
+        for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        s_next = mfma32<IsBf16>(kop[1], qop[1], s_next);
 #pragma unroll
-            for (int dt = 0; dt < 2; ++dt) {
-                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
-                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
-                const i16x8 vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                acc[dt] = mfma32<IsBf16>(vop, pop, acc[dt]);
+        for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        float l_a = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+            l_a = sum2<IsBf16>(pk[i], l_a);
+        }
+        if constexpr (!kMasked && !kExact) {
+            // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
+            // maximum over it and recompute. Rare.
+            if (__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum))) {
+                const float shift = exact_max(s_cur, 0, 8);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    s_cur[i] -= shift;
+                    s_next[i] -= shift;  // partial QK^T sum seeded with the old anchor
+                }
+                l_a = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
+                    l_a = sum2<IsBf16>(pk[i], l_a);
+                }
             }
         }
+        l_run += l_a;
+
+        // ---- block B: PV half 0, QK3, QK4 with exponentials of half 1
+        const i16x8 p0 = __builtin_bit_cast(i16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+        acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
+        acc[1] = mfma32<IsBf16>(vop[1], p0, acc[1]);
+        load_v(vb, g, 1, vop);
+        s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
+#pragma unroll
+        for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        s_next = mfma32<IsBf16>(kop[3], qop[3], s_next);
+#pragma unroll
+        for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (have_next) load_k(kn2, g2, kop);  // operands of the group after next
+        float l_b = 0.0f;
+#pragma unroll
+        for (int i = 4; i < 8; ++i) {
+            pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+            l_b = sum2<IsBf16>(pk[i], l_b);
+        }
+        if constexpr (!kMasked && !kExact) {
+            if (__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum))) {
+                const float shift = exact_max(s_cur, 8, 16);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    s_cur[i] -= shift;
+                    s_next[i] -= shift;
+                }
+                l_b = 0.0f;
+#pragma unroll
+                for (int i = 4; i < 8; ++i) {
+                    pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
+                    l_b = sum2<IsBf16>(pk[i], l_b);
+                }
+            }
+        }
+        l_run += l_b;
+
+        // ---- block C: PV half 1
+        const i16x8 p1 = __builtin_bit_cast(i16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
+        acc[0] = mfma32<IsBf16>(vop[0], p1, acc[0]);
+        acc[1] = mfma32<IsBf16>(vop[1], p1, acc[1]);
     };
 
-    // ---- main loop. Before tile t: K(t), K(t+1) and V(t) resident; tile t
-    // starts K(t+2) and V(t+1). sa/sb hold the scores of group 0 / group 1.
+    // ---- main loop. Step j = 2t + g handles key group g of tile t; it needs
+    // K operands of group j+1 (loaded in step j-1) and V(t), and prefetches the
+    // K operands of group j+2 from K(t+1). Tile t starts K(t+2), V(t+1): two K
+    // and two V buffers suffice. sa/sb: scores of groups 0/1.
     f32x16 sa, sb;
+    i16x8 kop[4];
     if (n_tiles > 0) {
         issue(0, 0);
         issue(1, -1);
         wait_vmem_all();
         __syncthreads();
-        sa = qk(kring[0], 0);
+        load_k(kring[0], 0, kop);
+        sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+        load_k(kring[0], 1, kop);
     }
-    auto tile = [&]<bool kMasked, bool kFirst>(int t) {
-        wait_vmem_all();
-        __syncthreads();
+    auto tile = [&]<bool kMasked, bool kFirst>(int t) __attribute__((always_inline)) {
+        wait_vmem_all();  // this lane's transfers of K(t+1), V(t) landed
+        __syncthreads();  // ... and every lane's; tile t-1 fully consumed
         uint64_t vis = ~0ull;
         if constexpr (kMasked) {
+            // vis bit j: key 64t + j exists and is not masked out (wave-uniform).
             const int key0 = t * kKeyTile;
             if (p.key_mask != nullptr) {
                 const int key = key0 + lane;
@@ -416,11 +479,11 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             if (key0 + kKeyTile > p.k_seq) vis &= (1ull << (p.k_seq - key0)) - 1ull;
         }
         issue(t + 2, t + 1);
-        const char* k_t = kring[t % kKRing];
-        const char* k_t1 = kring[(t + 1) % kKRing];
         const char* v_t = vring[t % kVRing];
-        group_step.template operator()<kMasked, kMasked || kFirst>(sa, sb, k_t, k_t, 1, v_t, 0, t, vis);
-        group_step.template operator()<kMasked, kMasked>(sb, sa, k_t, k_t1, 0, v_t, 1, t, vis);
+        const char* k_t1 = kring[(t + 1) % kKRing];
+        const bool more = t + 1 < n_tiles;
+        group_step.template operator()<kMasked, kMasked || kFirst>(sa, sb, kop, v_t, 0, t, vis, k_t1, 0, more);
+        group_step.template operator()<kMasked, kMasked>(sb, sa, kop, v_t, 1, t, vis, k_t1, 1, more);
     };
     int t = 0;
     if (n_plain > 0) {
