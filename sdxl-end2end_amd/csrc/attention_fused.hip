@@ -237,8 +237,9 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     // V (n >= 8); lane l takes row 8*(n%8) + l/8 and the global chunk
     // (l%8) ^ swz(row), which lands in its swizzled slot.
     // Issues the transfers of K tile kt and V tile vt (skipping tiles out of range).
-    // Per-lane offsets are recomputed per tile (a few ALU ops) rather than held
-    // in registers for the whole loop.
+    // Per-lane offsets are recomputed per tile with 24-bit multiplies (row
+    // strides are below 2^24 bytes, checked on the host) rather than held in
+    // registers; rows are clamped only in the partial last tile.
     auto issue = [&](int kt, int vt) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kLoadsPerWave; ++j) {
@@ -250,9 +251,9 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             const int64_t stride = is_v ? vs_bytes : ks_bytes;
             const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * stride;
             const int row = 8 * (n & 7) + (lane >> 3);
-            // partial tile: clamp rows to the last key
-            const int key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
-            const uint32_t off = (uint32_t)(key * stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            int key = row;
+            if (key0 + kKeyTile > p.k_seq) key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
+            const uint32_t off = __umul24((uint32_t)key, (uint32_t)stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
             const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
             lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
         }
@@ -416,7 +417,10 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
 #pragma unroll
         for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
-        if (have_next) load_k(kn2, g2, kop);  // operands of the group after next
+        // Operands of the group after next. Unconditional (stale data past the
+        // last tile is never used): a branch here would let the compiler sink
+        // the exponentials above past it and break the interleave.
+        load_k(kn2, g2, kop);
         float l_b = 0.0f;
 #pragma unroll
         for (int i = 4; i < 8; ++i) {
@@ -464,7 +468,9 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
         load_k(kring[0], 1, kop);
     }
-    auto tile = [&]<bool kMasked, bool kFirst>(int t) __attribute__((always_inline)) {
+    // kOdd: parity of t, so that every ring slot below is a compile-time
+    // offset (folded into the LDS instructions' immediates).
+    auto tile = [&]<bool kMasked, bool kFirst, bool kOdd>(int t) __attribute__((always_inline)) {
         wait_vmem_all();  // this lane's transfers of K(t+1), V(t) landed
         __syncthreads();  // ... and every lane's; tile t-1 fully consumed
         uint64_t vis = ~0ull;
@@ -479,18 +485,31 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             if (key0 + kKeyTile > p.k_seq) vis &= (1ull << (p.k_seq - key0)) - 1ull;
         }
         issue(t + 2, t + 1);
-        const char* v_t = vring[t % kVRing];
-        const char* k_t1 = kring[(t + 1) % kKRing];
-        const bool more = t + 1 < n_tiles;
-        group_step.template operator()<kMasked, kMasked || kFirst>(sa, sb, kop, v_t, 0, t, vis, k_t1, 0, more);
-        group_step.template operator()<kMasked, kMasked>(sb, sa, kop, v_t, 1, t, vis, k_t1, 1, more);
+        const char* v_t = vring[kOdd ? 1 : 0];
+        const char* k_t1 = kring[kOdd ? 0 : 1];
+        group_step.template operator()<kMasked, kMasked || kFirst>(sa, sb, kop, v_t, 0, t, vis, k_t1, 0, true);
+        group_step.template operator()<kMasked, kMasked>(sb, sa, kop, v_t, 1, t, vis, k_t1, 1, true);
     };
     int t = 0;
     if (n_plain > 0) {
-        tile.template operator()<false, true>(0);
-        for (t = 1; t < n_plain; ++t) tile.template operator()<false, false>(t);
+        tile.template operator()<false, true, false>(0);
+        for (t = 1; t + 1 < n_plain; t += 2) {
+            tile.template operator()<false, false, true>(t);
+            tile.template operator()<false, false, false>(t + 1);
+        }
+        if (t < n_plain) {
+            tile.template operator()<false, false, true>(t);
+            ++t;
+        }
     }
-    for (; t < n_tiles; ++t) tile.template operator()<true, false>(t);
+    if ((t & 1) && t < n_tiles) {
+        tile.template operator()<true, false, true>(t);
+        ++t;
+    }
+    for (; t < n_tiles; t += 2) {
+        tile.template operator()<true, false, false>(t);
+        if (t + 1 < n_tiles) tile.template operator()<true, false, true>(t + 1);
+    }
 
     // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
     // dims 32dt + 8u + 4hf + (0..3) of its query in acc[dt][4u .. 4u+3].

@@ -54,7 +54,8 @@ sdxl_status validate_desc(const sdxl_attn_desc* d) {
 }
 
 // Fused-kernel eligibility (pointer-independent part): fp16/bf16, head_dim 64,
-// every row stride a multiple of 8 elements (16-byte rows).
+// every row stride a multiple of 8 elements (16-byte rows) and below 2^23
+// elements (the kernel forms K/V row offsets with 24-bit multiplies).
 bool fused_shape_eligible(const sdxl_attn_desc* d) {
     if (d->dtype != SDXL_DTYPE_F16 && d->dtype != SDXL_DTYPE_BF16) return false;
     if (d->head_dim != 64) return false;
@@ -62,7 +63,7 @@ bool fused_shape_eligible(const sdxl_attn_desc* d) {
     const int64_t strides[4] = {eff_stride(d->q_row_stride, width), eff_stride(d->k_row_stride, width),
                                 eff_stride(d->v_row_stride, width), eff_stride(d->o_row_stride, width)};
     for (int64_t s : strides)
-        if (s % 8 != 0) return false;
+        if (s % 8 != 0 || s >= (int64_t{1} << 23)) return false;
     return true;
 }
 
