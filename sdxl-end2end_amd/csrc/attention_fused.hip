@@ -239,7 +239,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     // Issues the transfers of K tile kt and V tile vt (skipping tiles out of range).
     // Per-lane offsets are recomputed per tile with 24-bit multiplies (row
     // strides are below 2^24 bytes, checked on the host) rather than held in
-    // registers; rows are clamped only in the partial last tile.
+    // registers; rows past the end of a partial tile re-read the last key.
     auto issue = [&](int kt, int vt) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < kLoadsPerWave; ++j) {
@@ -251,8 +251,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             const int64_t stride = is_v ? vs_bytes : ks_bytes;
             const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * stride;
             const int row = 8 * (n & 7) + (lane >> 3);
-            int key = row;
-            if (key0 + kKeyTile > p.k_seq) key = key0 + row < p.k_seq ? row : p.k_seq - 1 - key0;
+            const int key = min(row, p.k_seq - 1 - key0);  // clamp rows of a partial tile
             const uint32_t off = __umul24((uint32_t)key, (uint32_t)stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
             const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
             lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
@@ -287,7 +286,10 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     float m_run = 0.0f;     // anchor, log2 units
     bool anchored = false;  // m_run came from a finite maximum
     float l_run = 0.0f;
-    f32x16 neg_m;           // -m_run in every entry: accumulator seed of QK^T
+    // Accumulator seed of QK^T: -m_run in every entry. Loop-carried; the
+    // rare anchor update rewrites it in place (tied asm operands) so that the
+    // join after that path needs no copies.
+    f32x16 neg_m;
 #pragma unroll
     for (int i = 0; i < 16; ++i) neg_m[i] = 0.0f;
 
@@ -328,8 +330,13 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
         l_run *= alpha;
         m_run += shift;
+        const float nm = -m_run;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) neg_m[i] = -m_run;
+        for (int i = 0; i < 16; ++i) {
+            float x = neg_m[i];
+            asm volatile("v_mov_b32 %0, %1" : "+v"(x) : "v"(nm));
+            neg_m[i] = x;
+        }
         return shift;
     };
 
