@@ -394,7 +394,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         if constexpr (!kMasked && !kExact) {
             // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
             // maximum over it and recompute. Rare.
-            if (__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum))) {
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum)) != 0, 0)) {
                 const float shift = exact_max(s_cur, 0, 8);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             l_b = sum2<IsBf16>(pk[i], l_b);
         }
         if constexpr (!kMasked && !kExact) {
-            if (__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum))) {
+            if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum)) != 0, 0)) {
                 const float shift = exact_max(s_cur, 8, 16);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
