@@ -36,7 +36,8 @@ typedef enum sdxl_status {
 typedef enum sdxl_dtype {
     SDXL_DTYPE_F16 = 0,
     SDXL_DTYPE_BF16 = 1,
-    SDXL_DTYPE_F32 = 2
+    SDXL_DTYPE_F32 = 2,
+    SDXL_DTYPE_E4M3 = 3 /* FP8 E4M3 (finite-only, bias 7): linear weights only */
 } sdxl_dtype;
 
 /* Backend selection. Values and accepted spellings mirror the reference's

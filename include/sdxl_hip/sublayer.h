@@ -1,0 +1,98 @@
+/* C ABI of the transformer attention sublayer on MI355X (gfx950).
+ *
+ * The reference's UNet transformer block runs, for its self-attention
+ * sublayer (src/cuda/unet.cpp:106-118):
+ *   normalized = Ops::layer_norm(hidden, norm1.weight, norm1.bias)     eps 1e-5
+ *   q, k, v    = Ops::linear(normalized, to_q / to_k / to_v.weight)     no bias
+ *   attention  = Ops::attention(q, k, v, heads)
+ *   attention  = Ops::linear(attention, to_out.0.weight, &to_out.0.bias)
+ *   Ops::add_in_place(hidden, attention)
+ * These entry points provide each step (sdxl_layer_norm, sdxl_linear) and the
+ * whole sublayer in one call (sdxl_attn_sublayer), with q/k/v as one fused
+ * projection against the row-concatenated weight [3W, W]. Linear weights are
+ * fp16 or FP8 E4M3 with per-output-channel fp32 scales (the reference's
+ * weight-only FP8 path, src/cuda/fp8_kernels.cu:52-245). fp32 accumulation,
+ * fp16 storage between steps. All calls are stream-ordered, allocate nothing
+ * and never synchronise. Errors as in attention.h (sdxl_last_error()).
+ */
+#ifndef SDXL_HIP_SUBLAYER_H
+#define SDXL_HIP_SUBLAYER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "attention.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* LayerNorm over the last dim (Ops::layer_norm, src/cuda/ops_kernels.cu:1428-1460;
+ * CPU semantics src/unet.cpp:237-263): y = (x - mean) / sqrt(var + eps) * gamma + beta,
+ * two-pass centred variance, fp16 x/gamma/beta/y, fp32 maths. width even, at most
+ * 2048 (SDXL: 320, 640, 1280, 2048). eps 0 means 1e-5. Row strides in
+ * elements (0 = width). y may equal x. */
+sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t x_row_stride,
+                            const void* gamma, const void* beta, float eps, void* y,
+                            int64_t y_row_stride, void* stream);
+
+typedef struct sdxl_linear_desc {
+    int64_t m; /* rows of a and c */
+    int64_t n; /* output features (rows of w) */
+    int64_t k; /* input features */
+    /* Row strides in elements; 0 means dense (k for a and w, n for c and residual). */
+    int64_t a_row_stride;
+    int64_t w_row_stride;
+    int64_t c_row_stride;
+    int64_t residual_row_stride;
+    int32_t w_dtype; /* SDXL_DTYPE_F16 or SDXL_DTYPE_E4M3; a, c, bias, residual are fp16 */
+    int32_t reserved; /* must be 0 */
+} sdxl_linear_desc;
+
+/* c = (a . w^T) * w_scale + bias + residual (Ops::linear, src/cuda/ops_blas.cpp;
+ * CPU semantics src/unet.cpp:202-222 plus add_in_place). w is [n, k] row-major
+ * (the reference's [out, in] storage). w_scale: per-output-channel fp32 scales,
+ * required for E4M3 weights (dequantised weight = code * scale), optional (NULL = 1)
+ * for fp16. bias [n] and residual [m, n] are optional (NULL). residual may equal c.
+ * Requires k % 64 == 0, n % 4 == 0, 16-byte aligned a/w rows and w_scale, 8-byte
+ * aligned c/bias/residual rows (SDXL widths all qualify). */
+sdxl_status sdxl_linear(const sdxl_linear_desc* desc, const void* a, const void* w, const float* w_scale,
+                        const void* bias, const void* residual, void* c, void* stream);
+
+/* Per-output-channel E4M3 quantisation of an fp16 weight [rows, cols] (the
+ * reference's FP8 weight packing, src/cuda/weights.cu:119-170): scale[r] =
+ * amax_r > 0 ? max(amax_r / 448, 1e-12) : 1 over finite values; q = E4M3(w / scale)
+ * rounded to nearest even, saturated to +-448. */
+sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, uint8_t* q, float* scales,
+                                    void* stream);
+
+typedef struct sdxl_sublayer_desc {
+    int64_t batch;
+    int64_t seq;
+    int64_t heads;     /* width = heads * 64 */
+    int32_t w_qkv_dtype; /* SDXL_DTYPE_F16 or SDXL_DTYPE_E4M3 */
+    int32_t attn_backend; /* sdxl_attn_backend for the attention step */
+    float ln_eps;      /* 0 means 1e-5 */
+    int32_t reserved;  /* must be 0 */
+} sdxl_sublayer_desc;
+
+/* Workspace the sublayer needs: batch * seq * width * 8 bytes (normalised
+ * hidden / attention output, then the fused q|k|v projection). */
+size_t sdxl_attn_sublayer_workspace_bytes(const sdxl_sublayer_desc* desc);
+
+/* y = x + to_out(attention(split_heads(LN(x) . w_qkv^T))) for hidden x [B, S, W]
+ * fp16: LayerNorm (gamma, beta [W]), fused q|k|v projection (w_qkv [3W, W] = to_q,
+ * to_k, to_v rows concatenated; w_qkv_scale [3W] for E4M3), head-dim-64 attention,
+ * output projection (w_out [W, W] fp16, b_out [W]) with the residual added in its
+ * epilogue. y may equal x. workspace: sdxl_attn_sublayer_workspace_bytes, 256-byte
+ * aligned. */
+sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* desc, const void* x, const void* ln_gamma,
+                               const void* ln_beta, const void* w_qkv, const float* w_qkv_scale,
+                               const void* w_out, const void* b_out, void* y, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SDXL_HIP_SUBLAYER_H */

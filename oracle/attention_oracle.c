@@ -407,3 +407,11 @@ void oracle_fp8_row_scales(const float* W, size_t out_features, size_t in_featur
         scales[o] = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
     }
 }
+
+/* Per-row E4M3 quantisation of W [rows, cols] (src/cuda/weights.cu:119-170):
+ * scales from oracle_fp8_row_scales, codes = oracle_float_to_e4m3(W / scale). */
+void oracle_quantize_e4m3_rows(const float* W, size_t rows, size_t cols, uint8_t* q, float* scales) {
+    oracle_fp8_row_scales(W, rows, cols, scales);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < cols; ++c) q[r * cols + c] = oracle_float_to_e4m3(W[r * cols + c] / scales[r]);
+}

@@ -68,6 +68,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_float_to_e4m3.argtypes = [ctypes.c_float]
         L.oracle_fp8_row_scales.restype = None
         L.oracle_fp8_row_scales.argtypes = [_f32p, _sz, _sz, _f32p]
+        L.oracle_quantize_e4m3_rows.restype = None
+        L.oracle_quantize_e4m3_rows.argtypes = [_f32p, _sz, _sz,
+                                                np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS"), _f32p]
         _lib = L
     return _lib
 
@@ -206,6 +209,21 @@ def fp8_row_scales(W) -> np.ndarray:
     s = np.empty(W.shape[0], dtype=np.float32)
     lib().oracle_fp8_row_scales(W, W.shape[0], W.shape[1], s)
     return s
+
+
+def quantize_e4m3_rows(W):
+    """(codes uint8 [rows, cols], scales fp32 [rows]) as the reference packs FP8 weights."""
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    q = np.empty(W.shape, dtype=np.uint8)
+    s = np.empty(W.shape[0], dtype=np.float32)
+    lib().oracle_quantize_e4m3_rows(W, W.shape[0], W.shape[1], q, s)
+    return q, s
+
+
+def dequantize_e4m3_rows(q, scales):
+    """W[r, c] = decode(q[r, c]) * scales[r] in fp32 (the CPU reference's FP8 weight read,
+    src/unet.cpp:91-119 plus the per-channel scale)."""
+    return e4m3_table()[np.asarray(q)] * np.asarray(scales, np.float32)[:, None]
 
 
 def error_stats(candidate, reference):

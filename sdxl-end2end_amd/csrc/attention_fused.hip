@@ -19,7 +19,7 @@
 //                             layout puts one query per lane column: row sums
 //                             stay in-lane (plus one lane<->lane+32 exchange).
 //   P = exp2(S)              v_exp_f32, packed to fp16/bf16 (v_cvt_pk_*),
-//                             summed with v_dot2 on the packed values.
+//                             row sums in fp32 (before rounding).
 //   O^T[d][q] += V^T P^T    : A = V^T built with ds_read_b64_tr_b16 straight
 //                             from the row-major V tile (no transpose pass),
 //                             B = P^T from the registers holding P.
@@ -119,16 +119,11 @@ __device__ __forceinline__ i16x8 scale_operand(i16x8 x, float c) {
     }
 }
 
-// Sum of the two packed values, added to acc in fp32.
-template <bool IsBf16>
-__device__ __forceinline__ float sum2(uint32_t packed, float acc) {
-    if constexpr (IsBf16) {
-        const uint32_t lo = packed << 16, hi = packed & 0xFFFF0000u;
-        return acc + __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
-    } else {
-        const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, packed), one, acc, false);
-    }
+// Sum of eight fp32 probabilities as a depth-3 tree. Plain fp32 adds: the
+// packed-dot (v_dot2) alternative shares issue resources with the matrix
+// cores and stalls them.
+__device__ __forceinline__ float sum8(const float* e) {
+    return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
 }
 
 // Exchange with lane l ^ 32 (the other half of the wave holds the other keys
@@ -375,23 +370,28 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         }
         float e[16];
         uint32_t pk[8];
+        constexpr bool kCheck = !kMasked && !kExact;
 
-        // ---- block A: QK1, QK2 with exponentials of half 0
+        // Eight slots, each one MFMA followed by about its duration (32 cycles)
+        // of VALU work that does not depend on it, pinned with scheduling
+        // barriers: the wave keeps issuing while the matrix core runs, and the
+        // dependent QK^T chain always has a slot between its links.
+        // 1: QK1 | exp 0-3
         s_next = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
         for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
+        // 2: QK2 | exp 4-7
         s_next = mfma32<IsBf16>(kop[1], qop[1], s_next);
 #pragma unroll
         for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
-        float l_a = 0.0f;
+        // 3: QK3 | pack + row sum of half 0, overflow check
+        s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-            l_a = sum2<IsBf16>(pk[i], l_a);
-        }
-        if constexpr (!kMasked && !kExact) {
+        for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+        float l_a = sum8(e);
+        if constexpr (kCheck) {
             // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
             // maximum over it and recompute. Rare.
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum)) != 0, 0)) {
@@ -401,40 +401,34 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
                     s_cur[i] -= shift;
                     s_next[i] -= shift;  // partial QK^T sum seeded with the old anchor
                 }
-                l_a = 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
-                    l_a = sum2<IsBf16>(pk[i], l_a);
-                }
+                for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+                l_a = sum8(e);
             }
         }
         l_run += l_a;
-
-        // ---- block B: PV half 0, QK3, QK4 with exponentials of half 1
-        const i16x8 p0 = __builtin_bit_cast(i16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
-        acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
-        acc[1] = mfma32<IsBf16>(vop[1], p0, acc[1]);
-        load_v(vb, g, 1, vop);
-        s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
+        __builtin_amdgcn_sched_barrier(0);
+        // 4: QK4 | exp 8-11
+        s_next = mfma32<IsBf16>(kop[3], qop[3], s_next);
 #pragma unroll
         for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
-        s_next = mfma32<IsBf16>(kop[3], qop[3], s_next);
+        // 5: PV half 0, d 0-31 | exp 12-15; K operands of the group after next
+        // (unconditional: stale data past the last tile is never used)
+        const i16x8 p0 = __builtin_bit_cast(i16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+        acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
 #pragma unroll
         for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
-        __builtin_amdgcn_sched_barrier(0);
-        // Operands of the group after next. Unconditional (stale data past the
-        // last tile is never used): a branch here would let the compiler sink
-        // the exponentials above past it and break the interleave.
         load_k(kn2, g2, kop);
-        float l_b = 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+        // 6: PV half 0, d 32-63 | pack + row sum of half 1, overflow check
+        acc[1] = mfma32<IsBf16>(vop[1], p0, acc[1]);
 #pragma unroll
-        for (int i = 4; i < 8; ++i) {
-            pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-            l_b = sum2<IsBf16>(pk[i], l_b);
-        }
-        if constexpr (!kMasked && !kExact) {
+        for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+        float l_b = sum8(e + 8);
+        if constexpr (kCheck) {
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum)) != 0, 0)) {
                 const float shift = exact_max(s_cur, 8, 16);
 #pragma unroll
@@ -442,20 +436,21 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
                     s_cur[i] -= shift;
                     s_next[i] -= shift;
                 }
-                l_b = 0.0f;
 #pragma unroll
-                for (int i = 4; i < 8; ++i) {
-                    pk[i] = pack2<IsBf16>(__builtin_amdgcn_exp2f(s_cur[2 * i]), __builtin_amdgcn_exp2f(s_cur[2 * i + 1]));
-                    l_b = sum2<IsBf16>(pk[i], l_b);
-                }
+                for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+#pragma unroll
+                for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
+                l_b = sum8(e + 8);
             }
         }
         l_run += l_b;
-
-        // ---- block C: PV half 1
+        load_v(vb, g, 1, vop);
+        __builtin_amdgcn_sched_barrier(0);
+        // 7, 8: PV half 1
         const i16x8 p1 = __builtin_bit_cast(i16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
         acc[0] = mfma32<IsBf16>(vop[0], p1, acc[0]);
         acc[1] = mfma32<IsBf16>(vop[1], p1, acc[1]);
+        (void)have_next;
     };
 
     // ---- main loop. Step j = 2t + g handles key group g of tile t; it needs

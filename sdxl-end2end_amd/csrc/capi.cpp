@@ -19,10 +19,16 @@ namespace {
 
 thread_local std::string g_last_error;
 
-sdxl_status fail(sdxl_status status, const std::string& message) {
+}  // namespace
+
+sdxl_status sdxl_hip_fail(sdxl_status status, const std::string& message) {
     g_last_error = message;
     return status;
 }
+
+namespace {
+
+sdxl_status fail(sdxl_status status, const std::string& message) { return sdxl_hip_fail(status, message); }
 
 int64_t eff_stride(int64_t stride, int64_t width) { return stride == 0 ? width : stride; }
 

@@ -1,0 +1,9 @@
+// Shared pieces of the C ABI translation units.
+#pragma once
+
+#include <string>
+
+#include "../../include/sdxl_hip/attention.h"
+
+// Records `message` as this thread's sdxl_last_error() and returns status.
+sdxl_status sdxl_hip_fail(sdxl_status status, const std::string& message);

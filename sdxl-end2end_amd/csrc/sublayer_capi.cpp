@@ -1,0 +1,176 @@
+// C ABI of the attention sublayer (include/sdxl_hip/sublayer.h): validation
+// and stream-ordered launches of LayerNorm, linear, E4M3 quantisation and the
+// whole LN -> fused QKV -> attention -> output projection + residual chain
+// (reference src/cuda/unet.cpp:106-118).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/sdxl_hip/sublayer.h"
+#include "capi_internal.hpp"
+#include "sublayer_kernels.hpp"
+
+namespace {
+
+bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
+
+sdxl_status launch_status(hipError_t err, const char* what) {
+    if (err != hipSuccess)
+        return sdxl_hip_fail(SDXL_STATUS_LAUNCH_FAILED, std::string(what) + ": " + hipGetErrorString(err));
+    return SDXL_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t x_row_stride, const void* gamma,
+                            const void* beta, float eps, void* y, int64_t y_row_stride, void* stream) {
+    // Message of the reference's Ops::layer_norm checks (ops_kernels.cu:1431-1437).
+    if (rows < 0 || width <= 0 || x_row_stride < 0 || y_row_stride < 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "CUDA layer norm shape/type mismatch");
+    const int64_t ldx = x_row_stride == 0 ? width : x_row_stride;
+    const int64_t ldy = y_row_stride == 0 ? width : y_row_stride;
+    if (ldx < width || ldy < width)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "CUDA layer norm shape/type mismatch");
+    if (width % 2 != 0 || width > 2048 || ldx % 2 != 0 || ldy % 2 != 0)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_layer_norm: width must be even and <= 2048");
+    if (rows == 0) return SDXL_STATUS_OK;
+    if (x == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm: null tensor pointer");
+    if (!aligned(x, 4) || !aligned(y, 4) || !aligned(gamma, 4) || !aligned(beta, 4))
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_layer_norm: tensors must be 4-byte aligned");
+    sdxl_hip::LayerNormParams p{};
+    p.x = x;
+    p.gamma = gamma;
+    p.beta = beta;
+    p.y = y;
+    p.rows = rows;
+    p.ldx = ldx;
+    p.ldy = ldy;
+    p.width = (int32_t)width;
+    p.eps = eps > 0.0f ? eps : 1.0e-5f;
+    return launch_status(sdxl_hip::launch_layer_norm(p, reinterpret_cast<hipStream_t>(stream)), "sdxl_layer_norm");
+}
+
+sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w, const float* w_scale,
+                        const void* bias, const void* residual, void* c, void* stream) {
+    if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: null descriptor");
+    if (d->reserved != 0) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: reserved field must be 0");
+    if (d->w_dtype != SDXL_DTYPE_F16 && d->w_dtype != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_linear: weights must be fp16 or E4M3");
+    if (d->m < 0 || d->n < 0 || d->k < 0 || d->m > INT32_MAX || d->n > INT32_MAX || d->k > INT32_MAX)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_linear: dimensions out of range");
+    const int64_t lda = d->a_row_stride ? d->a_row_stride : d->k;
+    const int64_t ldw = d->w_row_stride ? d->w_row_stride : d->k;
+    const int64_t ldc = d->c_row_stride ? d->c_row_stride : d->n;
+    const int64_t ldr = d->residual_row_stride ? d->residual_row_stride : d->n;
+    if (lda < d->k || ldw < d->k || ldc < d->n || ldr < d->n)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_linear: row stride smaller than the row");
+    const bool fp8 = d->w_dtype == SDXL_DTYPE_E4M3;
+    if (fp8 && w_scale == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "FP8 weight has invalid scaling metadata");
+    if (d->m == 0 || d->n == 0) return SDXL_STATUS_OK;
+    if (d->k % 64 != 0 || d->n % 4 != 0)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear: requires k % 64 == 0 and n % 4 == 0");
+    if (a == nullptr || w == nullptr || c == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: null tensor pointer");
+    const int64_t w_elem = fp8 ? 1 : 2;
+    if (!aligned(a, 16) || (lda * 2) % 16 != 0 || !aligned(w, 16) || (ldw * w_elem) % 16 != 0 ||
+        !aligned(c, 8) || ldc % 4 != 0 || (w_scale != nullptr && !aligned(w_scale, 16)) ||
+        (bias != nullptr && !aligned(bias, 8)) || (residual != nullptr && (!aligned(residual, 8) || ldr % 4 != 0)))
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear: misaligned tensor or row stride");
+    if (lda * 2 * 128 > UINT32_MAX || ldw * w_elem * 128 > UINT32_MAX)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear: row stride too large");
+    sdxl_hip::LinearParams p{};
+    p.a = a;
+    p.w = w;
+    p.w_scale = w_scale;
+    p.bias = bias;
+    p.residual = residual;
+    p.c = c;
+    p.lda = lda;
+    p.ldw = ldw;
+    p.ldr = ldr;
+    p.ldc = ldc;
+    p.m = (int32_t)d->m;
+    p.n = (int32_t)d->n;
+    p.k = (int32_t)d->k;
+    return launch_status(sdxl_hip::launch_linear(p, fp8, reinterpret_cast<hipStream_t>(stream)), "sdxl_linear");
+}
+
+sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, uint8_t* q, float* scales,
+                                    void* stream) {
+    if (rows < 0 || cols < 0) return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_quantize_e4m3_rows: negative shape");
+    if (rows == 0) return SDXL_STATUS_OK;
+    if (w == nullptr || q == nullptr || scales == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_quantize_e4m3_rows: null tensor pointer");
+    if (!aligned(w, 2) || !aligned(scales, 4))
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_quantize_e4m3_rows: misaligned tensor");
+    sdxl_hip::QuantizeParams p{};
+    p.w = w;
+    p.q = q;
+    p.scales = scales;
+    p.rows = rows;
+    p.cols = cols;
+    return launch_status(sdxl_hip::launch_quantize_e4m3_rows(p, reinterpret_cast<hipStream_t>(stream)),
+                         "sdxl_quantize_e4m3_rows");
+}
+
+size_t sdxl_attn_sublayer_workspace_bytes(const sdxl_sublayer_desc* d) {
+    if (d == nullptr || d->batch < 0 || d->seq < 0 || d->heads < 0) return 0;
+    return (size_t)d->batch * (size_t)d->seq * (size_t)(d->heads * 64) * 8u;
+}
+
+sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const void* ln_gamma, const void* ln_beta,
+                               const void* w_qkv, const float* w_qkv_scale, const void* w_out, const void* b_out,
+                               void* y, void* workspace, size_t workspace_bytes, void* stream) {
+    if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: null descriptor");
+    if (d->reserved != 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: reserved field must be 0");
+    if (d->batch < 0 || d->seq < 0 || d->heads <= 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_attn_sublayer: invalid shape");
+    const int64_t W = d->heads * 64;
+    const int64_t M = d->batch * d->seq;
+    if (M == 0) return SDXL_STATUS_OK;
+    if (workspace == nullptr || workspace_bytes < sdxl_attn_sublayer_workspace_bytes(d) || !aligned(workspace, 256))
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: workspace missing, small or misaligned");
+    char* ws = static_cast<char*>(workspace);
+    void* hidden_ws = ws;                                  // [M, W]: LN output, later attention output
+    void* qkv = ws + (size_t)M * (size_t)W * 2;            // [M, 3W]
+
+    sdxl_status st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+    if (st != SDXL_STATUS_OK) return st;
+
+    sdxl_linear_desc qd{};
+    qd.m = M;
+    qd.n = 3 * W;
+    qd.k = W;
+    qd.w_dtype = d->w_qkv_dtype;
+    st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+    if (st != SDXL_STATUS_OK) return st;
+
+    sdxl_attn_desc ad{};
+    ad.batch = d->batch;
+    ad.q_seq = d->seq;
+    ad.k_seq = d->seq;
+    ad.heads = d->heads;
+    ad.head_dim = 64;
+    ad.q_row_stride = ad.k_row_stride = ad.v_row_stride = 3 * W;
+    ad.o_row_stride = W;
+    ad.dtype = SDXL_DTYPE_F16;
+    ad.backend = d->attn_backend;
+    const char* qkv_c = static_cast<const char*>(qkv);
+    st = sdxl_attn_fwd(&ad, qkv_c, qkv_c + W * 2, qkv_c + 2 * W * 2, nullptr, hidden_ws, stream);
+    if (st != SDXL_STATUS_OK) return st;
+
+    sdxl_linear_desc od{};
+    od.m = M;
+    od.n = W;
+    od.k = W;
+    od.w_dtype = SDXL_DTYPE_F16;
+    return sdxl_linear(&od, hidden_ws, w_out, nullptr, b_out, x, y, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// Internal launch interface of the sublayer kernels (sublayer.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sdxl_hip {
+
+// c[m, n] = w_scale[n] * sum_k a[m, k] * w[n, k] + bias[n] + residual[m, n]
+// a, c, bias, residual fp16; w fp16 or E4M3 codes; strides in elements.
+// Requires k % 64 == 0, n % 4 == 0, 16-byte aligned a/w rows, 8-byte
+// aligned c/bias/residual rows, 16-byte aligned w_scale.
+struct LinearParams {
+    const void* a;
+    const void* w;
+    const float* w_scale;   // nullable: 1
+    const void* bias;       // nullable
+    const void* residual;   // nullable
+    void* c;
+    int64_t lda, ldw, ldr, ldc;
+    int32_t m, n, k;
+    int32_t m_blocks, n_blocks;  // filled by the launcher
+};
+hipError_t launch_linear(const LinearParams& params, bool w_fp8, hipStream_t stream);
+
+struct LayerNormParams {
+    const void* x;
+    const void* gamma;
+    const void* beta;
+    void* y;
+    int64_t rows;
+    int64_t ldx, ldy;
+    int32_t width;  // even, <= 2048
+    float eps;
+};
+hipError_t launch_layer_norm(const LayerNormParams& params, hipStream_t stream);
+
+struct QuantizeParams {
+    const void* w;   // fp16 [rows, cols]
+    uint8_t* q;      // E4M3 [rows, cols]
+    float* scales;   // [rows]
+    int64_t rows, cols;
+};
+hipError_t launch_quantize_e4m3_rows(const QuantizeParams& params, hipStream_t stream);
+
+}  // namespace sdxl_hip

@@ -1,4 +1,4 @@
-"""Python harness binding of the sdxl_hip attention C ABI (include/sdxl_hip/attention.h).
+"""Python harness binding of the sdxl_hip C ABI (include/sdxl_hip/attention.h, sublayer.h).
 
 This is a thin ctypes layer used by the test suite, the smoke check and bench.py.
 Device memory and streams come from PyTorch (plumbing only); every computation
@@ -16,7 +16,7 @@ LIB_PATH = os.environ.get("SDXL_HIP_LIB") or os.path.join(PKG_ROOT, "lib", "libs
 # sdxl_status
 OK, INVALID_ARGUMENT, INVALID_SHAPE, UNSUPPORTED, LAUNCH_FAILED, DEVICE_ERROR = range(6)
 # sdxl_dtype
-F16, BF16, F32 = 0, 1, 2
+F16, BF16, F32, E4M3 = 0, 1, 2, 3
 # sdxl_attn_backend (values of the reference's AttentionBackend, runtime.hpp:53-58)
 AUTO, CUDNN_SDPA, FLASH_SM80, WARP_ONLINE = 0, 1, 2, 3
 
@@ -29,6 +29,11 @@ EXPORTED_SYMBOLS = (
     "sdxl_status_string",
     "sdxl_last_error",
     "sdxl_abi_version",
+    "sdxl_layer_norm",
+    "sdxl_linear",
+    "sdxl_quantize_e4m3_rows",
+    "sdxl_attn_sublayer_workspace_bytes",
+    "sdxl_attn_sublayer",
 )
 
 
@@ -51,6 +56,22 @@ class AttnDesc(ctypes.Structure):
         ("reserved", ctypes.c_int32),
         ("scale", ctypes.c_float),
     ]
+
+
+class LinearDesc(ctypes.Structure):
+    """Mirror of struct sdxl_linear_desc."""
+
+    _fields_ = [(n, ctypes.c_int64) for n in ("m", "n", "k", "a_row_stride", "w_row_stride",
+                                              "c_row_stride", "residual_row_stride")] + \
+               [("w_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class SublayerDesc(ctypes.Structure):
+    """Mirror of struct sdxl_sublayer_desc."""
+
+    _fields_ = [("batch", ctypes.c_int64), ("seq", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("w_qkv_dtype", ctypes.c_int32), ("attn_backend", ctypes.c_int32),
+                ("ln_eps", ctypes.c_float), ("reserved", ctypes.c_int32)]
 
 
 class SdxlError(RuntimeError):
@@ -90,6 +111,18 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sdxl_last_error.argtypes = []
     lib.sdxl_abi_version.restype = ctypes.c_int32
     lib.sdxl_abi_version.argtypes = []
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    lib.sdxl_layer_norm.restype = ctypes.c_int
+    lib.sdxl_layer_norm.argtypes = [i64, i64, vp, i64, vp, vp, ctypes.c_float, vp, i64, vp]
+    lib.sdxl_linear.restype = ctypes.c_int
+    lib.sdxl_linear.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp]
+    lib.sdxl_quantize_e4m3_rows.restype = ctypes.c_int
+    lib.sdxl_quantize_e4m3_rows.argtypes = [i64, i64, vp, vp, vp, vp]
+    lib.sdxl_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
+    lib.sdxl_attn_sublayer_workspace_bytes.argtypes = [ctypes.POINTER(SublayerDesc)]
+    lib.sdxl_attn_sublayer.restype = ctypes.c_int
+    lib.sdxl_attn_sublayer.argtypes = [ctypes.POINTER(SublayerDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                       ctypes.c_size_t, vp]
     _LIB = lib
     return lib
 
@@ -184,3 +217,84 @@ def attention_bytes(batch: int, heads: int, q_seq: int, k_seq: int, head_dim: in
                     elem: int = 2) -> float:
     """Algorithmic HBM bytes of one call: Q, K, V read once and O written once."""
     return float(elem) * batch * heads * head_dim * (2 * q_seq + 2 * k_seq)
+
+
+# ---------------------------------------------------------------- attention sublayer
+# (include/sdxl_hip/sublayer.h; reference src/cuda/unet.cpp:106-118)
+
+def _stream(t) -> int:
+    import torch
+    return torch.cuda.current_stream(t.device).cuda_stream if t.is_cuda else 0
+
+
+def _ptr(t) -> int:
+    return t.data_ptr() if t is not None else 0
+
+
+def layer_norm(x, gamma, beta, eps: float = 1e-5, out=None):
+    """Ops::layer_norm (reference src/cuda/ops_kernels.cu:1428-1460) on fp16 [..., W] tensors."""
+    import torch
+    if out is None:
+        out = torch.empty_like(x)
+    W = x.shape[-1]
+    rows = x.numel() // W if W else 0
+    _check(load().sdxl_layer_norm(rows, W, _ptr(x), x.stride(-2) if x.dim() > 1 else W, _ptr(gamma),
+                                  _ptr(beta), eps, _ptr(out), out.stride(-2) if out.dim() > 1 else W,
+                                  _stream(x)))
+    return out
+
+
+def linear(a, w, w_scale=None, bias=None, residual=None, out=None):
+    """Ops::linear: a [M, K] fp16, w [N, K] fp16 or uint8 E4M3 codes (with w_scale [N] fp32),
+    optional bias [N] and residual [M, N]; returns [M, N] fp16 (2-D views with unit column stride)."""
+    import torch
+    M, K = a.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    d = LinearDesc(m=M, n=N, k=K, a_row_stride=a.stride(0), w_row_stride=w.stride(0),
+                   c_row_stride=out.stride(0),
+                   residual_row_stride=residual.stride(0) if residual is not None else 0,
+                   w_dtype=E4M3 if w.dtype == torch.uint8 else F16, reserved=0)
+    _check(load().sdxl_linear(ctypes.byref(d), _ptr(a), _ptr(w), _ptr(w_scale), _ptr(bias), _ptr(residual),
+                              _ptr(out), _stream(a)))
+    return out
+
+
+def quantize_e4m3_rows(w):
+    """Per-output-channel E4M3 weight quantisation (reference src/cuda/weights.cu:119-170):
+    returns (codes uint8 [N, K], scales fp32 [N])."""
+    import torch
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.uint8, device=w.device)
+    s = torch.empty((N,), dtype=torch.float32, device=w.device)
+    _check(load().sdxl_quantize_e4m3_rows(N, K, _ptr(w.contiguous()), _ptr(q), _ptr(s), _stream(w)))
+    return q, s
+
+
+def sublayer_workspace_bytes(batch: int, seq: int, heads: int) -> int:
+    return int(load().sdxl_attn_sublayer_workspace_bytes(ctypes.byref(SublayerDesc(batch=batch, seq=seq,
+                                                                                   heads=heads))))
+
+
+def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads: int, out=None,
+                  workspace=None, backend: int = AUTO, eps: float = 0.0):
+    """x + to_out(attention(LN(x) . w_qkv^T)) for hidden x [B, S, W] fp16 (reference
+    src/cuda/unet.cpp:106-118 with q/k/v fused): w_qkv [3W, W] fp16 or uint8 E4M3 + w_qkv_scale [3W]."""
+    import torch
+    B, S, W = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    d = SublayerDesc(batch=B, seq=S, heads=heads, w_qkv_dtype=E4M3 if w_qkv.dtype == torch.uint8 else F16,
+                     attn_backend=backend, ln_eps=eps, reserved=0)
+    nbytes = int(load().sdxl_attn_sublayer_workspace_bytes(ctypes.byref(d)))
+    if workspace is None:
+        workspace = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)
+    _check(load().sdxl_attn_sublayer(ctypes.byref(d), _ptr(x), _ptr(ln_gamma), _ptr(ln_beta), _ptr(w_qkv),
+                                     _ptr(w_qkv_scale), _ptr(w_out), _ptr(b_out), _ptr(out), _ptr(workspace),
+                                     workspace.numel(), _stream(x)))
+    return out
+
+
+def linear_flops(m: int, n: int, k: int) -> float:
+    return 2.0 * m * n * k

@@ -1,5 +1,5 @@
 """Host-only checks of the C ABI (no GPU work): the library loads, exports every
-function include/sdxl_hip/attention.h declares, and reproduces the reference's
+function include/sdxl_hip/attention.h and sublayer.h declare, and reproduces the reference's
 backend spellings, eligibility rules and error behaviour
 (src/cuda/runtime.cpp:61-87, src/cuda/ops_kernels.cu:1912-1952)."""
 import os
@@ -11,11 +11,11 @@ import pytest
 import sdxl_hip as sh
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "sdxl_hip", "attention.h")
+HEADERS = [os.path.join(ROOT, "include", "sdxl_hip", h) for h in ("attention.h", "sublayer.h")]
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = "\n".join(open(h).read() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(sdxl_\w+)\s*\(", text, re.M)))
 
 
@@ -145,3 +145,52 @@ def test_torch_wrapper_shape_checks():
         sh.attention(q, k, k, 3)
     with pytest.raises(sh.SdxlError, match="key mask mismatch"):
         sh.attention(q, k, k, 1, key_mask=torch.ones(1, 8, dtype=torch.int64))
+
+
+# ---------------------------------------------------------------- sublayer entry points (validation only)
+
+def _lin(m=8, n=8, k=64, w_dtype=sh.F16, **kw):
+    return sh.LinearDesc(m=m, n=n, k=k, w_dtype=w_dtype, **kw)
+
+
+def _lin_status(d, a=16, w=16, scale=0, bias=0, res=0, c=16):
+    import ctypes
+    return sh.load().sdxl_linear(ctypes.byref(d), a, w, scale or None, bias or None, res or None, c, None)
+
+
+def test_linear_validation():
+    assert _lin_status(_lin(w_dtype=sh.BF16)) == sh.INVALID_SHAPE
+    assert _lin_status(_lin(reserved=1)) == sh.INVALID_ARGUMENT
+    assert _lin_status(_lin(w_dtype=sh.E4M3)) == sh.INVALID_ARGUMENT          # E4M3 needs scales
+    assert "scaling metadata" in sh.load().sdxl_last_error().decode()
+    assert _lin_status(_lin(k=80)) == sh.UNSUPPORTED                          # k % 64
+    assert _lin_status(_lin(n=6)) == sh.UNSUPPORTED                           # n % 4
+    assert _lin_status(_lin(a_row_stride=32)) == sh.INVALID_SHAPE             # stride < k
+    assert _lin_status(_lin(), a=8) == sh.UNSUPPORTED                         # misaligned a
+    assert _lin_status(_lin(), w=0) == sh.INVALID_ARGUMENT                    # null weight
+    assert _lin_status(_lin(m=0)) == sh.OK                                    # empty: nothing to do
+
+
+def test_layer_norm_validation():
+    L = sh.load()
+    assert L.sdxl_layer_norm(4, 101, 16, 0, 16, 16, 0.0, 16, 101, None) == sh.UNSUPPORTED
+    assert L.sdxl_layer_norm(4, 4096, 16, 0, 16, 16, 0.0, 16, 0, None) == sh.UNSUPPORTED
+    assert L.sdxl_layer_norm(-1, 640, 16, 0, 16, 16, 0.0, 16, 0, None) == sh.INVALID_SHAPE
+    assert sh.load().sdxl_last_error().decode() == "CUDA layer norm shape/type mismatch"
+    assert L.sdxl_layer_norm(4, 640, 16, 320, 16, 16, 0.0, 16, 0, None) == sh.INVALID_SHAPE
+    assert L.sdxl_layer_norm(0, 640, 0, 0, 0, 0, 0.0, 0, 0, None) == sh.OK
+    assert L.sdxl_layer_norm(4, 640, 0, 0, 16, 16, 0.0, 16, 0, None) == sh.INVALID_ARGUMENT
+
+
+def test_sublayer_workspace_and_validation():
+    import ctypes
+    assert sh.sublayer_workspace_bytes(2, 4096, 10) == 2 * 4096 * 640 * 8
+    d = sh.SublayerDesc(batch=2, seq=64, heads=2)
+    L = sh.load()
+    args = [16] * 7
+    assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, None, 1 << 20, None) == sh.INVALID_ARGUMENT
+    assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1024, None) == sh.INVALID_ARGUMENT  # too small
+    d.reserved = 1
+    assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1 << 20, None) == sh.INVALID_ARGUMENT
+    assert L.sdxl_quantize_e4m3_rows(-1, 4, 16, 16, 16, None) == sh.INVALID_SHAPE
+    assert L.sdxl_quantize_e4m3_rows(0, 4, 0, 0, 0, None) == sh.OK

@@ -73,6 +73,29 @@ def test_e4m3_code_points():
     assert oracle.lib().oracle_float_to_e4m3(1.0625) == 0x38       # tie 1.0/1.125 -> even mantissa
 
 
+def test_quantize_e4m3_rows_round_trip_bound():
+    """Codes of the row quantiser: the row's amax maps to +-448 (code 0x7E/0xFE), and every
+    dequantised weight is the nearest E4M3 grid point (error <= half the local spacing)."""
+    W = oracle.normal_f32(901, (37, 640), 0.02)
+    W[3, 5] = 0.0
+    W[4, :] = 0.0  # all-zero row: scale 1, codes 0
+    q, s = oracle.quantize_e4m3_rows(W)
+    np.testing.assert_array_equal(s, oracle.fp8_row_scales(W))
+    assert (q[4] == 0).all() and s[4] == 1.0
+    t = oracle.e4m3_table()
+    for r in (0, 1, 36):
+        c = int(np.argmax(np.abs(W[r])))
+        assert q[r, c] in (0x7E, 0xFE)
+    x = W / s[:, None]
+    deq = t[q]
+    grid = np.sort(np.unique(np.abs(t[~np.isnan(t)])))
+    idx = np.clip(np.searchsorted(grid, np.abs(x)), 1, len(grid) - 1)
+    spacing = grid[idx] - grid[idx - 1]
+    assert (np.abs(deq - x) <= spacing / 2 + 1e-12).all()
+    np.testing.assert_array_equal(np.sign(deq[deq != 0]), np.sign(x[deq != 0]))
+    np.testing.assert_allclose(oracle.dequantize_e4m3_rows(q, s), deq * s[:, None])
+
+
 def test_fp8_row_scales_rule():
     W = np.array([[0.0, 0.0], [1.0, -896.0], [1e-14, 0.0]], np.float32)
     s = oracle.fp8_row_scales(W)
