@@ -39,7 +39,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c5...) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -74,6 +74,71 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
     return wall_ms, kernel_ms, out
+
+
+def time_fn(torch, fn, steps, warmup):
+    """Mean device ms of fn() from per-launch events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        starts[i].record(stream)
+        fn()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
+
+
+def bench_sublayer(torch, sh, steps=50, warmup=5):
+    """hidden [2, 4096, 640] -> LayerNorm -> fused QKV with E4M3 weights [1920, 640] and
+    per-channel scales (absmax/448, N(0, 0.02) init) -> 10-head attention -> fp16 out-proj [640, 640]
+    + bias + residual. Per-stage device time and the fused sdxl_attn_sublayer call."""
+    B, S, H = 2, 4096, 10
+    W, M = H * 64, B * S
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(7)
+    x = torch.randn(B, S, W, device="cuda:0", generator=g).half()
+    gamma = torch.ones(W, dtype=torch.float16, device="cuda:0")
+    beta = torch.zeros(W, dtype=torch.float16, device="cuda:0")
+    w_qkv = (torch.randn(3 * W, W, device="cuda:0", generator=g) * 0.02).half()
+    q8, s8 = sh.quantize_e4m3_rows(w_qkv)
+    w_out = (torch.randn(W, W, device="cuda:0", generator=g) * 0.02).half()
+    b_out = (torch.randn(W, device="cuda:0", generator=g) * 0.02).half()
+    n = torch.empty_like(x)
+    qkv = torch.empty(M, 3 * W, dtype=torch.float16, device="cuda:0")
+    attn = torch.empty(B, S, W, dtype=torch.float16, device="cuda:0")
+    y = torch.empty_like(x)
+    q3 = qkv.view(B, S, 3 * W)
+    ws = torch.empty(sh.sublayer_workspace_bytes(B, S, H), dtype=torch.uint8, device="cuda:0")
+    stages = {
+        "layer_norm": (lambda: sh.layer_norm(x, gamma, beta, out=n), 0.0, 4.0 * M * W),
+        "qkv_e4m3": (lambda: sh.linear(n.view(M, W), q8, w_scale=s8, out=qkv), sh.linear_flops(M, 3 * W, W),
+                     2.0 * M * W + 3 * W * W + 2.0 * M * 3 * W),
+        "attention": (lambda: sh.attention(q3[..., :W], q3[..., W:2 * W], q3[..., 2 * W:], H, out=attn),
+                      sh.attention_flops(B, H, S, S), sh.attention_bytes(B, H, S, S)),
+        "out_proj_bias_residual": (lambda: sh.linear(attn.view(M, W), w_out, bias=b_out, residual=x.view(M, W),
+                                                     out=y.view(M, W)),
+                                   sh.linear_flops(M, W, W), 2.0 * M * W * 3 + 2.0 * W * W),
+    }
+    out = {"shape": [B, S, W], "heads": H, "w_qkv": "E4M3 [1920, 640] per-channel scales", "stages": {}}
+    total = 0.0
+    for name, (fn, fl, by) in stages.items():
+        ms = time_fn(torch, fn, steps, warmup)
+        total += ms
+        e = {"us": round(ms * 1e3, 2), "hbm_gbs": round(by / (ms * 1e-3) / 1e9, 1),
+             "hbm_frac": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        if fl:
+            e["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+            e["mfma_frac"] = round(fl / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
+        out["stages"][name] = e
+    ms = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws),
+                 steps, warmup)
+    out["sum_of_stages_us"] = round(total * 1e3, 2)
+    out["fused_call_us"] = round(ms * 1e3, 2)
+    return out
 
 
 def read_traffic():
@@ -148,6 +213,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         return
+    if args.only == "c4":
+        print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)
@@ -203,6 +271,7 @@ def main():
                          "hbm_gbs": round(by / (k_ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
             del qq, kk, vv
+        sec["c4_sublayer"] = bench_sublayer(torch, sh)
         result["secondary"] = sec
 
     if not args.no_cpu:

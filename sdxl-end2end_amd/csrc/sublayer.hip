@@ -37,8 +37,9 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr int kBM = 128, kBN = 128, kBK = 64;
@@ -72,8 +73,6 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
         : "v"(voff), "s"(base), "s"(lds));
 }
 
-__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
-
 // Four E4M3 codes -> four fp16 values (exact).
 __device__ __forceinline__ uint2 e4m3x4_to_f16(uint32_t x) {
     const f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(x, 1.0f, false);
@@ -81,10 +80,26 @@ __device__ __forceinline__ uint2 e4m3x4_to_f16(uint32_t x) {
     return uint2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
 }
 
-template <bool kWFp8>
-__global__ __launch_bounds__(256, 2) void linear_kernel(LinearParams p) {
-    __shared__ __attribute__((aligned(16))) char abuf[2][kTileBytes];
-    __shared__ __attribute__((aligned(16))) char wbuf[2][kTileBytes];
+// s_waitcnt vmcnt(n) (lgkmcnt(0), expcnt untouched) for a compile-time n < 64.
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
+}
+
+// kRing LDS stages of kBK = 64 columns of K; stage s + kRing - 1 is requested
+// while stage s is consumed (prefetch distance kRing - 1 stages), so that a
+// stage's transfers have several stages of MFMA work to land. E4M3 weights
+// stay as codes in LDS (64-byte rows, chunk swizzle (row >> 2) & 3) and are
+// decoded when the operand is read; fp16 weights use the A-operand layout.
+template <bool kWFp8, int kRing, int kOcc>
+__global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
+    constexpr int kWRowBytes = kWFp8 ? 64 : kRowBytes;
+    constexpr int kWTileBytes = 128 * kWRowBytes;
+    constexpr int kLoadsPerStage = 4 + (kWFp8 ? 2 : 4);  // 1-KiB transfers per wave and stage
+    // Stage st: A tile at smem[st], W tile right after it. The epilogue
+    // reuses the whole array.
+    __shared__ __attribute__((aligned(16))) char smem[kRing][kTileBytes + kWTileBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -105,55 +120,57 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(LinearParams p) {
     const int m0 = mb * kBM, n0 = nb * kBN;
     const int n_stages = p.k / kBK;
 
-    const char* abase = (const char*)p.a;
-    const char* wbase = (const char*)p.w;
+    const char* abase = (const char*)p.a + (int64_t)m0 * p.lda * 2;
     const int64_t lda_b = p.lda * 2;
     const int64_t ldw_b = kWFp8 ? p.ldw : p.ldw * 2;
+    const char* wbase = (const char*)p.w + (int64_t)n0 * ldw_b;
+    const int a_rows = p.m - 1 - m0, w_rows = p.n - 1 - n0;  // last valid tile row
 
-    // ---- stage loads. A (and fp16 W): 16 1-KiB transfers per operand and
-    // stage, 4 per wave; transfer n covers tile rows 8n .. 8n+7, lane l the
-    // row 8n + l/8 and global chunk (l%8) ^ swz(row), landing in its slot.
-    auto issue_dma = [&](const char* gbase, int64_t ld_b, int row0, int rows, int k0, char* buf)
-                         __attribute__((always_inline)) {
+    // Epilogue column constants, loaded now so that their latency hides under
+    // the main loop: lane l finishes columns 4(l%16) .. +3 of its wave block.
+    const int wm = (threadIdx.x >> 6) & 1, wn = threadIdx.x >> 7;
+    const int ec = lane & 15;
+    const int en = n0 + wn * 64 + 4 * ec;
+    const bool en_ok = en < p.n;
+    float4 e_scale = {1.0f, 1.0f, 1.0f, 1.0f}, e_bias = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (en_ok && p.w_scale != nullptr) e_scale = *(const float4*)(p.w_scale + en);
+    if (en_ok && p.bias != nullptr) {
+        const f16x4 bb = *(const f16x4*)((const _Float16*)p.bias + en);
+        e_bias = float4{(float)bb[0], (float)bb[1], (float)bb[2], (float)bb[3]};
+    }
+
+    // ---- stage transfers (rows past the end re-read the last row).
+    // 128-byte rows (A, fp16 W): transfer n covers rows 8n .. 8n+7; lane l
+    // takes row 8n + l/8 and global chunk (l%8) ^ swz(row), its slot's chunk.
+    auto dma_rows128 = [&](const char* gbase, int64_t ld_b, int last, int kbyte, char* buf, int n)
+                           __attribute__((always_inline)) {
+        const int row = 8 * n + (lane >> 3);
+        const uint32_t off = (uint32_t)(min(row, last) * ld_b) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+        lds_dma16(gbase + kbyte, off, lds_addr(buf + 8 * n * kRowBytes));
+    };
+    // 64-byte rows (E4M3 W): transfer n covers rows 16n .. 16n+15; lane l takes
+    // row 16n + l/4 and global chunk (l%4) ^ ((row >> 2) & 3).
+    auto dma_rows64 = [&](int kbyte, char* buf, int n) __attribute__((always_inline)) {
+        const int row = 16 * n + (lane >> 2);
+        const uint32_t off = (uint32_t)(min(row, w_rows) * ldw_b) + (uint32_t)(((lane & 3) ^ ((row >> 2) & 3)) << 4);
+        lds_dma16(wbase + kbyte, off, lds_addr(buf + 16 * n * 64));
+    };
+    auto issue_stage = [&](int st) __attribute__((always_inline)) {
+        char* ab = smem[st % kRing];
+        char* wb = smem[st % kRing] + kTileBytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = wave * 4 + j;
-            const int row = 8 * n + (lane >> 3);
-            const int lrow = min(row, rows - 1 - row0);  // rows past the end re-read the last row
-            const char* tile_base = gbase + (int64_t)row0 * ld_b + (int64_t)k0 * 2;
-            const uint32_t off = (uint32_t)(lrow * ld_b) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-            lds_dma16(tile_base, off, lds_addr(buf + 8 * n * kRowBytes));
-        }
-    };
-    // E4M3 W: thread t loads 32 codes (row t/2, k half t%2) into registers ...
-    const int wq_row = threadIdx.x >> 1, wq_half = threadIdx.x & 1;
-    const char* wq_src = wbase + (int64_t)min(n0 + wq_row, p.n - 1) * ldw_b + wq_half * 32;
-    u32x4 wq[2];
-    auto load_wq = [&](int k0) __attribute__((always_inline)) {
-        const u32x4* src = (const u32x4*)(wq_src + k0);
-        wq[0] = src[0];
-        wq[1] = src[1];
-    };
-    // ... and stores them decoded as four 16-byte chunks of its tile row.
-    auto store_wq = [&](char* buf) __attribute__((always_inline)) {
-        char* row = buf + wq_row * kRowBytes;
-        const int s = swz(wq_row);
+        for (int j = 0; j < 4; ++j) dma_rows128(abase, lda_b, a_rows, st * kBK * 2, ab, wave * 4 + j);
+        if constexpr (kWFp8) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint2 lo = e4m3x4_to_f16(wq[c >> 1][2 * (c & 1)]);
-            const uint2 hi = e4m3x4_to_f16(wq[c >> 1][2 * (c & 1) + 1]);
-            *(lds_u32x4*)(row + (((4 * wq_half + c) ^ s) << 4)) = u32x4{lo.x, lo.y, hi.x, hi.y};
+            for (int j = 0; j < 2; ++j) dma_rows64(st * kBK, wb, wave * 2 + j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dma_rows128(wbase, ldw_b, w_rows, st * kBK * 2, wb, wave * 4 + j);
         }
-    };
-    auto issue_stage = [&](int s) __attribute__((always_inline)) {
-        issue_dma(abase, lda_b, m0, p.m, s * kBK, abuf[s & 1]);
-        if constexpr (kWFp8) load_wq(s * kBK);
-        else issue_dma(wbase, ldw_b, n0, p.n, s * kBK, wbuf[s & 1]);
     };
 
     // ---- wave block: 64 (M) x 64 (N) at (wm, wn); acc[j][i] = C^T tile of
     // n-tile j and m-tile i.
-    const int wm = wave & 1, wn = wave >> 1;
     f32x16 acc[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -161,77 +178,106 @@ __global__ __launch_bounds__(256, 2) void linear_kernel(LinearParams p) {
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-    int a_off[2], w_off[2];
+    int a_off[2], a_swz[2], w_off[2], w_swz[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int ar = wm * 64 + 32 * t + col, wr = wn * 64 + 32 * t + col;
         a_off[t] = ar * kRowBytes;
-        w_off[t] = wr * kRowBytes;
+        a_swz[t] = swz(ar);
+        w_off[t] = wr * kWRowBytes + (kWFp8 ? hf * 8 : 0);
+        w_swz[t] = kWFp8 ? (wr >> 2) & 3 : swz(wr);
     }
-    const int a_swz[2] = {swz(wm * 64 + col), swz(wm * 64 + 32 + col)};
-    const int w_swz[2] = {swz(wn * 64 + col), swz(wn * 64 + 32 + col)};
 
-    issue_stage(0);
-    if constexpr (kWFp8) {
-        store_wq(wbuf[0]);
-    }
-    wait_vmem_all();
-    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < kRing - 1; ++st)
+        if (st < n_stages) issue_stage(st);
     for (int s = 0; s < n_stages; ++s) {
-        const bool more = s + 1 < n_stages;
-        if (more) issue_stage(s + 1);
-        const char* ab = abuf[s & 1];
-        const char* wb = wbuf[s & 1];
+        // Stage s landed (this wave's transfers; later stages may still fly) ...
+        const int later = min(n_stages - 1 - s, kRing - 2);
+        if constexpr (kRing >= 4) {
+            if (later >= 2) wait_vmem<2 * kLoadsPerStage>();
+            else if (later == 1) wait_vmem<kLoadsPerStage>();
+            else wait_vmem<0>();
+        } else if constexpr (kRing == 3) {
+            if (later >= 1) wait_vmem<kLoadsPerStage>();
+            else wait_vmem<0>();
+        } else {
+            wait_vmem<0>();
+        }
+        __syncthreads();  // ... for every wave, and stage s - 1's buffers are free
+        if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
+        const char* ab = smem[s % kRing];
+        const char* wb = smem[s % kRing] + kTileBytes;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             i16x8 aop[2], wop[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 aop[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
-                wop[t] = *(const lds_i16x8*)(wb + w_off[t] + (((2 * ks + hf) ^ w_swz[t]) << 4));
+                if constexpr (kWFp8) {
+                    const u32x2 raw = *(const lds_u32x2*)(wb + w_off[t] + ((ks ^ w_swz[t]) << 4));
+                    const uint2 lo = e4m3x4_to_f16(raw[0]), hi = e4m3x4_to_f16(raw[1]);
+                    wop[t] = __builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                } else {
+                    wop[t] = *(const lds_i16x8*)(wb + w_off[t] + (((2 * ks + hf) ^ w_swz[t]) << 4));
+                }
             }
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int i = 0; i < 2; ++i) acc[j][i] = mfma32(wop[j], aop[i], acc[j][i]);
         }
-        if constexpr (kWFp8) {
-            if (more) store_wq(wbuf[(s + 1) & 1]);
-        }
-        wait_vmem_all();
-        __syncthreads();
     }
 
-    // ---- epilogue. acc[j][i][4u + q]: output row m = m0 + wm*64 + 32i + col,
-    // column n = n0 + wn*64 + 32j + 8u + 4hf + q.
+    // ---- epilogue, through LDS so that HBM sees whole rows: each wave parks
+    // its 64 x 64 fp32 block row-major (256-byte rows, 16-byte chunk c of row r
+    // at c ^ (r & 15): conflict-free for 16 lanes of distinct rows), then
+    // reads it back: lane l owns columns 4(l%16) .. +3 of rows 4it + l/16, so
+    // residual loads and output stores are 128-byte row segments per 16
+    // lanes. All 16 residual loads are issued before the staging so that one
+    // round trip covers them. acc[j][i][4u + q] is row 32i + col, column
+    // 32j + 8u + 4hf + q of the wave block.
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+    const int rm0 = m0 + wm * 64 + (lane >> 4);  // row of iteration it: rm0 + 4 it
+    f16x4 res[16];
+    if (p.residual != nullptr && en_ok) {
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const int m = min(rm0 + 4 * it, p.m - 1);
+            res[it] = *(const f16x4*)((const _Float16*)p.residual + (int64_t)m * p.ldr + en);
+        }
+    } else {
+#pragma unroll
+        for (int it = 0; it < 16; ++it) res[it] = f16x4{0, 0, 0, 0};
+    }
+    __syncthreads();  // every wave is done with the stage buffers
+    char* eb = &smem[0][0] + wave * (64 * 256);
+    static_assert(sizeof(smem) >= 4 * 64 * 256, "epilogue staging fits in the stage buffers");
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int m = m0 + wm * 64 + 32 * i + col;
-        if (m >= p.m) continue;
+        const int r = 32 * i + col;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int n = n0 + wn * 64 + 32 * j + 8 * u + 4 * hf;
-                if (n >= p.n) continue;
-                float v[4] = {acc[j][i][4 * u], acc[j][i][4 * u + 1], acc[j][i][4 * u + 2], acc[j][i][4 * u + 3]};
-                if (p.w_scale != nullptr) {
-                    const float4 sc = *(const float4*)(p.w_scale + n);
-                    v[0] *= sc.x, v[1] *= sc.y, v[2] *= sc.z, v[3] *= sc.w;
-                }
-                if (p.bias != nullptr) {
-                    const f16x4 bb = *(const f16x4*)((const _Float16*)p.bias + n);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) v[q] += (float)bb[q];
-                }
-                if (p.residual != nullptr) {
-                    const f16x4 rr = *(const f16x4*)((const _Float16*)p.residual + (int64_t)m * p.ldr + n);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) v[q] += (float)rr[q];
-                }
-                const f16x4 out = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-                *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + n) = out;
+                const int c = 8 * j + 2 * u + hf;
+                *(lds_f32x4*)(eb + r * 256 + ((c ^ (r & 15)) << 4)) =
+                    f32x4{acc[j][i][4 * u], acc[j][i][4 * u + 1], acc[j][i][4 * u + 2], acc[j][i][4 * u + 3]};
             }
+    }
+    if (!en_ok) return;
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+        const int r = 4 * it + (lane >> 4);
+        const int m = rm0 + 4 * it;
+        if (m >= p.m) break;
+        const f32x4 a = *(const lds_f32x4*)(eb + r * 256 + ((ec ^ (r & 15)) << 4));
+        const float v0 = a[0] * e_scale.x + e_bias.x + (float)res[it][0];
+        const float v1 = a[1] * e_scale.y + e_bias.y + (float)res[it][1];
+        const float v2 = a[2] * e_scale.z + e_bias.z + (float)res[it][2];
+        const float v3 = a[3] * e_scale.w + e_bias.w + (float)res[it][3];
+        *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en) = f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
     }
 }
 
@@ -329,8 +375,8 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, hipStream_t 
     if (tasks == 0) return hipSuccess;
     if (tasks > 0x7FFFFFFF || p.k % kBK != 0 || p.n % 4 != 0) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(256);
-    if (w_fp8) hipLaunchKernelGGL(linear_kernel<true>, grid, block, 0, stream, p);
-    else hipLaunchKernelGGL(linear_kernel<false>, grid, block, 0, stream, p);
+    if (w_fp8) hipLaunchKernelGGL((linear_kernel<true, 3, 2>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((linear_kernel<false, 2, 2>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
