@@ -76,26 +76,37 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     return wall_ms, kernel_ms, out
 
 
-def time_fn(torch, fn, steps, warmup):
-    """Mean device ms of fn() from per-launch events on the current stream."""
+def time_fn(torch, fn, steps, warmup, reps=10):
+    """Device us per call of fn(), host launch cost excluded: `reps` calls captured in one HIP
+    graph (the C ABI calls are capturable), the graph replayed `steps` times between events."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for i in range(steps):
-        starts[i].record(stream)
-        fn()
-        ends[i].record(stream)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(reps):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
-    return sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (steps * reps)
 
 
 def bench_sublayer(torch, sh, steps=50, warmup=5):
     """hidden [2, 4096, 640] -> LayerNorm -> fused QKV with E4M3 weights [1920, 640] and
     per-channel scales (absmax/448, N(0, 0.02) init) -> 10-head attention -> fp16 out-proj [640, 640]
-    + bias + residual. Per-stage device time and the fused sdxl_attn_sublayer call."""
+    + bias + residual. Per-stage device time and the fused sdxl_attn_sublayer call, both from
+    captured-graph replays (host launch cost excluded)."""
     B, S, H = 2, 4096, 10
     W, M = H * 64, B * S
     g = torch.Generator(device="cuda:0")
@@ -123,7 +134,8 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
                                                      out=y.view(M, W)),
                                    sh.linear_flops(M, W, W), 2.0 * M * W * 3 + 2.0 * W * W),
     }
-    out = {"shape": [B, S, W], "heads": H, "w_qkv": "E4M3 [1920, 640] per-channel scales", "stages": {}}
+    out = {"shape": [B, S, W], "heads": H, "w_qkv": "E4M3 [1920, 640] per-channel scales",
+           "timing": "device us per call, HIP graph replay", "stages": {}}
     total = 0.0
     for name, (fn, fl, by) in stages.items():
         ms = time_fn(torch, fn, steps, warmup)

@@ -42,9 +42,8 @@ typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) char lds_char;
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kBN = 128, kBK = 64;
 constexpr int kRowBytes = kBK * 2;              // 128: one fp16 tile row
-constexpr int kTileBytes = 128 * kRowBytes;     // 16 KiB
 
 __device__ __forceinline__ int rev3(int x) { return ((x & 1) << 2) | (x & 2) | ((x >> 2) & 1); }
 __device__ __forceinline__ int swz(int row) { return rev3((row >> 1) & 7); }
@@ -87,19 +86,25 @@ __device__ __forceinline__ void wait_vmem() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
 }
 
-// kRing LDS stages of kBK = 64 columns of K; stage s + kRing - 1 is requested
-// while stage s is consumed (prefetch distance kRing - 1 stages), so that a
-// stage's transfers have several stages of MFMA work to land. E4M3 weights
-// stay as codes in LDS (64-byte rows, chunk swizzle (row >> 2) & 3) and are
-// decoded when the operand is read; fp16 weights use the A-operand layout.
-template <bool kWFp8, int kRing, int kOcc>
+// One workgroup = 4 waves in a 2 x 2 arrangement = a (64 kTM) x 128 output
+// tile; each wave computes (32 kTM) x 64 as kTM x 2 MFMA tiles. kRing LDS
+// stages of kBK = 64 columns of K: stage s + kRing - 1 is requested while
+// stage s is consumed (prefetch distance kRing - 1 stages), so that a stage's
+// transfers have MFMA work to land behind. E4M3 weights stay as codes in LDS
+// (64-byte rows, chunk swizzle (row >> 2) & 3) and are decoded when the
+// operand is read; fp16 weights use the A-operand layout.
+template <bool kWFp8, int kTM, int kRing, int kOcc>
 __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
+    constexpr int kBMt = 64 * kTM;
     constexpr int kWRowBytes = kWFp8 ? 64 : kRowBytes;
+    constexpr int kATileBytes = kBMt * kRowBytes;
     constexpr int kWTileBytes = 128 * kWRowBytes;
-    constexpr int kLoadsPerStage = 4 + (kWFp8 ? 2 : 4);  // 1-KiB transfers per wave and stage
+    constexpr int kAXfers = kBMt / 32;               // 1-KiB A transfers per wave and stage
+    constexpr int kWXfers = kWFp8 ? 2 : 4;
+    constexpr int kLoadsPerStage = kAXfers + kWXfers;
     // Stage st: A tile at smem[st], W tile right after it. The epilogue
-    // reuses the whole array.
-    __shared__ __attribute__((aligned(16))) char smem[kRing][kTileBytes + kWTileBytes];
+    // reuses the array.
+    __shared__ __attribute__((aligned(16))) char smem[kRing][kATileBytes + kWTileBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
         task = xcd * per + (xcd < extra ? xcd : extra) + slot;
     }
     const int mb = task / p.n_blocks, nb = task % p.n_blocks;
-    const int m0 = mb * kBM, n0 = nb * kBN;
+    const int m0 = mb * kBMt, n0 = nb * kBN;
     const int n_stages = p.k / kBK;
 
     const char* abase = (const char*)p.a + (int64_t)m0 * p.lda * 2;
@@ -128,7 +133,7 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
 
     // Epilogue column constants, loaded now so that their latency hides under
     // the main loop: lane l finishes columns 4(l%16) .. +3 of its wave block.
-    const int wm = (threadIdx.x >> 6) & 1, wn = threadIdx.x >> 7;
+    const int wm = wave & 1, wn = wave >> 1;
     const int ec = lane & 15;
     const int en = n0 + wn * 64 + 4 * ec;
     const bool en_ok = en < p.n;
@@ -157,33 +162,37 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     };
     auto issue_stage = [&](int st) __attribute__((always_inline)) {
         char* ab = smem[st % kRing];
-        char* wb = smem[st % kRing] + kTileBytes;
+        char* wb = smem[st % kRing] + kATileBytes;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma_rows128(abase, lda_b, a_rows, st * kBK * 2, ab, wave * 4 + j);
+        for (int j = 0; j < kAXfers; ++j) dma_rows128(abase, lda_b, a_rows, st * kBK * 2, ab, wave * kAXfers + j);
         if constexpr (kWFp8) {
 #pragma unroll
-            for (int j = 0; j < 2; ++j) dma_rows64(st * kBK, wb, wave * 2 + j);
+            for (int j = 0; j < kWXfers; ++j) dma_rows64(st * kBK, wb, wave * kWXfers + j);
         } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dma_rows128(wbase, ldw_b, w_rows, st * kBK * 2, wb, wave * 4 + j);
+            for (int j = 0; j < kWXfers; ++j) dma_rows128(wbase, ldw_b, w_rows, st * kBK * 2, wb, wave * kWXfers + j);
         }
     };
 
-    // ---- wave block: 64 (M) x 64 (N) at (wm, wn); acc[j][i] = C^T tile of
-    // n-tile j and m-tile i.
-    f32x16 acc[2][2];
+    // ---- wave block: rows wm*32kTM .. +32kTM, columns wn*64 .. +64;
+    // acc[j][i] = C^T tile of n-tile j and m-tile i.
+    f32x16 acc[2][kTM];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < kTM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-    int a_off[2], a_swz[2], w_off[2], w_swz[2];
+    int a_off[kTM], a_swz[kTM], w_off[2], w_swz[2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int ar = wm * 64 + 32 * t + col, wr = wn * 64 + 32 * t + col;
+    for (int t = 0; t < kTM; ++t) {
+        const int ar = wm * 32 * kTM + 32 * t + col;
         a_off[t] = ar * kRowBytes;
         a_swz[t] = swz(ar);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int wr = wn * 64 + 32 * t + col;
         w_off[t] = wr * kWRowBytes + (kWFp8 ? hf * 8 : 0);
         w_swz[t] = kWFp8 ? (wr >> 2) & 3 : swz(wr);
     }
@@ -207,13 +216,12 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
         __syncthreads();  // ... for every wave, and stage s - 1's buffers are free
         if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
         const char* ab = smem[s % kRing];
-        const char* wb = smem[s % kRing] + kTileBytes;
+        const char* wb = smem[s % kRing] + kATileBytes;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            i16x8 aop[2], wop[2];
+            i16x8 aop[kTM], wop[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                aop[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
                 if constexpr (kWFp8) {
                     const u32x2 raw = *(const lds_u32x2*)(wb + w_off[t] + ((ks ^ w_swz[t]) << 4));
                     const uint2 lo = e4m3x4_to_f16(raw[0]), hi = e4m3x4_to_f16(raw[1]);
@@ -223,61 +231,65 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
+            for (int t = 0; t < kTM; ++t)
+                aop[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
 #pragma unroll
-                for (int i = 0; i < 2; ++i) acc[j][i] = mfma32(wop[j], aop[i], acc[j][i]);
+            for (int i = 0; i < kTM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[j][i] = mfma32(wop[j], aop[i], acc[j][i]);
         }
     }
 
-    // ---- epilogue, through LDS so that HBM sees whole rows: each wave parks
-    // its 64 x 64 fp32 block row-major (256-byte rows, 16-byte chunk c of row r
-    // at c ^ (r & 15): conflict-free for 16 lanes of distinct rows), then
-    // reads it back: lane l owns columns 4(l%16) .. +3 of rows 4it + l/16, so
-    // residual loads and output stores are 128-byte row segments per 16
-    // lanes. All 16 residual loads are issued before the staging so that one
-    // round trip covers them. acc[j][i][4u + q] is row 32i + col, column
-    // 32j + 8u + 4hf + q of the wave block.
+    // ---- epilogue, one m-tile (32 rows) at a time through LDS so that HBM
+    // sees whole rows: the wave parks the tile's 32 x 64 fp32 block row-major
+    // (256-byte rows, 16-byte chunk c of row r at c ^ (r & 15): conflict-free
+    // for 16 lanes of distinct rows), then reads it back with lane l owning
+    // columns 4(l%16) .. +3 of rows 4it + l/16: residual loads and output
+    // stores are 128-byte row segments per 16 lanes. The tile's 8 residual
+    // loads are all issued before its staging. acc[j][i][4u + q] is row
+    // 32i + col, column 32j + 8u + 4hf + q of the wave block.
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
-    const int rm0 = m0 + wm * 64 + (lane >> 4);  // row of iteration it: rm0 + 4 it
-    f16x4 res[16];
-    if (p.residual != nullptr && en_ok) {
-#pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const int m = min(rm0 + 4 * it, p.m - 1);
-            res[it] = *(const f16x4*)((const _Float16*)p.residual + (int64_t)m * p.ldr + en);
-        }
-    } else {
-#pragma unroll
-        for (int it = 0; it < 16; ++it) res[it] = f16x4{0, 0, 0, 0};
-    }
+    char* eb = &smem[0][0] + wave * (32 * 256);
+    static_assert(sizeof(smem) >= 4 * 32 * 256, "epilogue staging fits in the stage buffers");
     __syncthreads();  // every wave is done with the stage buffers
-    char* eb = &smem[0][0] + wave * (64 * 256);
-    static_assert(sizeof(smem) >= 4 * 64 * 256, "epilogue staging fits in the stage buffers");
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 32 * i + col;
+    for (int i = 0; i < kTM; ++i) {
+        const int rm0 = m0 + wm * 32 * kTM + 32 * i + (lane >> 4);  // row of iteration it: rm0 + 4 it
+        f16x4 res[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it) res[it] = f16x4{0, 0, 0, 0};
+        if (p.residual != nullptr && en_ok) {
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int m = min(rm0 + 4 * it, p.m - 1);
+                res[it] = *(const f16x4*)((const _Float16*)p.residual + (int64_t)m * p.ldr + en);
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int c = 8 * j + 2 * u + hf;
-                *(lds_f32x4*)(eb + r * 256 + ((c ^ (r & 15)) << 4)) =
+                *(lds_f32x4*)(eb + col * 256 + ((c ^ (col & 15)) << 4)) =
                     f32x4{acc[j][i][4 * u], acc[j][i][4 * u + 1], acc[j][i][4 * u + 2], acc[j][i][4 * u + 3]};
             }
-    }
-    if (!en_ok) return;
+        if (en_ok) {
 #pragma unroll
-    for (int it = 0; it < 16; ++it) {
-        const int r = 4 * it + (lane >> 4);
-        const int m = rm0 + 4 * it;
-        if (m >= p.m) break;
-        const f32x4 a = *(const lds_f32x4*)(eb + r * 256 + ((ec ^ (r & 15)) << 4));
-        const float v0 = a[0] * e_scale.x + e_bias.x + (float)res[it][0];
-        const float v1 = a[1] * e_scale.y + e_bias.y + (float)res[it][1];
-        const float v2 = a[2] * e_scale.z + e_bias.z + (float)res[it][2];
-        const float v3 = a[3] * e_scale.w + e_bias.w + (float)res[it][3];
-        *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en) = f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+            for (int it = 0; it < 8; ++it) {
+                const int r = 4 * it + (lane >> 4);
+                const int m = rm0 + 4 * it;
+                if (m < p.m) {
+                    const f32x4 a = *(const lds_f32x4*)(eb + r * 256 + ((ec ^ (r & 15)) << 4));
+                    const float v0 = a[0] * e_scale.x + e_bias.x + (float)res[it][0];
+                    const float v1 = a[1] * e_scale.y + e_bias.y + (float)res[it][1];
+                    const float v2 = a[2] * e_scale.z + e_bias.z + (float)res[it][2];
+                    const float v3 = a[3] * e_scale.w + e_bias.w + (float)res[it][3];
+                    *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en) =
+                        f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+                }
+            }
+        }
     }
 }
 
@@ -288,12 +300,31 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
 // reference's block reduction by rounding only).
 constexpr int kLnMaxPer = 16;  // half2 pairs per lane: width <= 2048
 
+// Sum over the wave: DPP butterflies inside each 16-lane row (quad_perm
+// [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror pair every lane with one
+// from the other half at each level), then the four row sums through
+// readlane. Result in every lane.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_pair_add(float x) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false);
+    return x + __builtin_bit_cast(float, moved);
+}
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, 64);
-    return x;
+    x = dpp_pair_add<0xB1>(x);   // quad_perm [1,0,3,2]
+    x = dpp_pair_add<0x4E>(x);   // quad_perm [2,3,0,1]
+    x = dpp_pair_add<0x141>(x);  // row_half_mirror
+    x = dpp_pair_add<0x140>(x);  // row_mirror
+    const int b = __builtin_bit_cast(int, x);
+    return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
 }
 
+// kPer fp16 pairs per lane (width <= 128 kPer): straight-line code, every
+// load issued before the first use (indices clamped, values masked), so one
+// memory round trip covers the row.
+template <int kPer>
 __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -302,22 +333,23 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     const f16x2* x = (const f16x2*)((const _Float16*)p.x + row * p.ldx);
     const f16x2* g = (const f16x2*)p.gamma;
     const f16x2* bt = (const f16x2*)p.beta;
-    float v[2 * kLnMaxPer];
+    f16x2 h[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) h[j] = x[min(lane + 64 * j, pairs - 1)];
+    float v[2 * kPer];
     float sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        if (lane + 64 * j < pairs) {
-            const f16x2 h = x[lane + 64 * j];
-            v[2 * j] = (float)h[0];
-            v[2 * j + 1] = (float)h[1];
-            sum += v[2 * j] + v[2 * j + 1];
-        }
+    for (int j = 0; j < kPer; ++j) {
+        const bool ok = lane + 64 * j < pairs;
+        v[2 * j] = ok ? (float)h[j][0] : 0.0f;
+        v[2 * j + 1] = ok ? (float)h[j][1] : 0.0f;
+        sum += v[2 * j] + v[2 * j + 1];
     }
     const float inv_w = 1.0f / (float)p.width;
     const float mean = wave_sum(sum) * inv_w;
     float sq = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
+    for (int j = 0; j < kPer; ++j) {
         if (lane + 64 * j < pairs) {
             const float d0 = v[2 * j] - mean, d1 = v[2 * j + 1] - mean;
             sq += d0 * d0 + d1 * d1;
@@ -327,9 +359,9 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     const float inv = 1.0f / sqrtf(var + p.eps);
     f16x2* y = (f16x2*)((_Float16*)p.y + row * p.ldy);
 #pragma unroll
-    for (int j = 0; j < kLnMaxPer; ++j) {
-        if (lane + 64 * j < pairs) {
-            const int c = lane + 64 * j;
+    for (int j = 0; j < kPer; ++j) {
+        const int c = lane + 64 * j;
+        if (c < pairs) {
             const f16x2 gg = g[c], bb = bt[c];
             const float y0 = (v[2 * j] - mean) * inv * (float)gg[0] + (float)bb[0];
             const float y1 = (v[2 * j + 1] - mean) * inv * (float)gg[1] + (float)bb[1];
@@ -367,24 +399,40 @@ __global__ __launch_bounds__(256) void quantize_e4m3_rows_kernel(QuantizeParams 
 
 }  // namespace
 
-hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, hipStream_t stream) {
+hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_units, hipStream_t stream) {
     LinearParams p = params_in;
-    p.m_blocks = (p.m + kBM - 1) / kBM;
+    if (p.m == 0 || p.n == 0) return hipSuccess;
+    if (p.k % kBK != 0 || p.n % 4 != 0) return hipErrorInvalidValue;
     p.n_blocks = (p.n + kBN - 1) / kBN;
+    // 256-row tiles (twice the MFMA work per staged byte) when they still give
+    // at least 80% of the resident workgroups (two per CU) work; else 128.
+    const int64_t tall = (int64_t)((p.m + 255) / 256) * p.n_blocks;
+    const bool use_tall = w_fp8 && tall * 5 >= (int64_t)compute_units * 2 * 4;
+    p.m_blocks = use_tall ? (p.m + 255) / 256 : (p.m + 127) / 128;
     const int64_t tasks = (int64_t)p.m_blocks * p.n_blocks;
-    if (tasks == 0) return hipSuccess;
-    if (tasks > 0x7FFFFFFF || p.k % kBK != 0 || p.n % 4 != 0) return hipErrorInvalidValue;
+    if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(256);
-    if (w_fp8) hipLaunchKernelGGL((linear_kernel<true, 3, 2>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((linear_kernel<false, 2, 2>), grid, block, 0, stream, p);
+    if (w_fp8) {
+        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, 4, 2, 2>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((linear_kernel<true, 2, 3, 2>), grid, block, 0, stream, p);
+    } else {
+        hipLaunchKernelGGL((linear_kernel<false, 2, 2, 2>), grid, block, 0, stream, p);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_layer_norm(const LayerNormParams& p, hipStream_t stream) {
     if (p.rows == 0) return hipSuccess;
-    if (p.width % 2 != 0 || p.width > 128 * kLnMaxPer) return hipErrorInvalidValue;
+    if (p.width % 2 != 0 || p.width <= 0 || p.width > 128 * kLnMaxPer) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
-    hipLaunchKernelGGL(layer_norm_kernel, grid, block, 0, stream, p);
+    switch ((p.width + 127) / 128) {
+#define SDXL_LN_CASE(n) \
+    case n: hipLaunchKernelGGL(layer_norm_kernel<n>, grid, block, 0, stream, p); break;
+        SDXL_LN_CASE(1) SDXL_LN_CASE(2) SDXL_LN_CASE(3) SDXL_LN_CASE(4) SDXL_LN_CASE(5) SDXL_LN_CASE(6)
+        SDXL_LN_CASE(7) SDXL_LN_CASE(8) SDXL_LN_CASE(9) SDXL_LN_CASE(10) SDXL_LN_CASE(11) SDXL_LN_CASE(12)
+        SDXL_LN_CASE(13) SDXL_LN_CASE(14) SDXL_LN_CASE(15) SDXL_LN_CASE(16)
+#undef SDXL_LN_CASE
+    }
     return hipGetLastError();
 }
 

@@ -15,6 +15,19 @@ namespace {
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
+// CUs of the current device, cached per device (0 if unknown).
+int compute_units() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+        cached[dev] = cus > 0 ? cus : -1;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
 sdxl_status launch_status(hipError_t err, const char* what) {
     if (err != hipSuccess)
         return sdxl_hip_fail(SDXL_STATUS_LAUNCH_FAILED, std::string(what) + ": " + hipGetErrorString(err));
@@ -97,7 +110,7 @@ sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w,
     p.m = (int32_t)d->m;
     p.n = (int32_t)d->n;
     p.k = (int32_t)d->k;
-    return launch_status(sdxl_hip::launch_linear(p, fp8, reinterpret_cast<hipStream_t>(stream)), "sdxl_linear");
+    return launch_status(sdxl_hip::launch_linear(p, fp8, compute_units(), reinterpret_cast<hipStream_t>(stream)), "sdxl_linear");
 }
 
 sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, uint8_t* q, float* scales,

@@ -21,7 +21,8 @@ struct LinearParams {
     int32_t m, n, k;
     int32_t m_blocks, n_blocks;  // filled by the launcher
 };
-hipError_t launch_linear(const LinearParams& params, bool w_fp8, hipStream_t stream);
+// compute_units: CUs of the device (tile-size choice).
+hipError_t launch_linear(const LinearParams& params, bool w_fp8, int compute_units, hipStream_t stream);
 
 struct LayerNormParams {
     const void* x;

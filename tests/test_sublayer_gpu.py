@@ -119,7 +119,7 @@ def test_linear_fp16_bias_residual(M, N, K):
     within_half_ulp(plain, _linear_ref(ab, oracle.f16_bits_to_f32(wb)), 1e-4, "linear fp16 plain")
 
 
-@pytest.mark.parametrize("M", [8192, 333])
+@pytest.mark.parametrize("M", [8192, 8100, 333])
 def test_linear_e4m3_qkv(M):
     """configs[3] fused QKV projection: [M, 640] x E4M3 [1920, 640] with per-row scales."""
     K, N = 640, 1920
