@@ -1,6 +1,8 @@
 // Operator layer of the sdxl_hip C++20 host API: the attention entry point of
-// the reference's Ops (include/sdxl/cuda/ops.hpp:92-97), implemented over the
-// C ABI sdxl_attn_fwd (include/sdxl_hip/attention.h).
+// the reference's Ops (include/sdxl/cuda/ops.hpp:92-97) and the operators of
+// the UNet transformer block's attention sublayer (layer_norm, linear with
+// fp16 or FP8 E4M3 weights, FP8 weight packing), implemented over the C ABI
+// (include/sdxl_hip/attention.h, sublayer.h).
 #pragma once
 
 #include "sdxl_hip/runtime.hpp"
@@ -25,6 +27,36 @@ public:
     // Same computation into a caller-owned output (no allocation at all).
     void attention_into(const Tensor& query, const Tensor& key, const Tensor& value, std::size_t heads,
                         Tensor& output, bool causal = false, const Tensor* key_mask = nullptr) const;
+
+    // LayerNorm over the last dim (reference Ops::layer_norm, ops_kernels.cu:1428-1460):
+    // fp16 input [..., W], weight/bias [W]; W even, <= 2048.
+    [[nodiscard]] Tensor layer_norm(const Tensor& input, const Tensor& weight, const Tensor& bias,
+                                    float epsilon = 1.0e-5F) const;
+
+    // input . weight^T + bias (reference Ops::linear): fp16 input [..., K], weight [N, K]
+    // fp16 or Float8E4M3 with attached per-output-channel scales (pack_e4m3), optional
+    // fp16 bias [N]. K % 64 == 0, N % 4 == 0.
+    [[nodiscard]] Tensor linear(const Tensor& input, const Tensor& weight, const Tensor* bias = nullptr) const;
+
+    // hidden += input . weight^T + bias in one pass (the reference's linear followed by
+    // add_in_place, unet.cpp:114-118, with the residual added in the linear's epilogue).
+    void linear_residual_into(const Tensor& input, const Tensor& weight, const Tensor* bias, Tensor& hidden) const;
+
+    // Per-output-channel E4M3 packing of an fp16 weight [N, K] (reference
+    // src/cuda/weights.cu:119-170): returns the codes with their scales attached.
+    [[nodiscard]] Tensor pack_e4m3(const Tensor& weight) const;
+
+    // Rows of q, k, v projection weights [W, W] concatenated into [3W, W]
+    // (fp16), the fused QKV weight attention_sublayer takes.
+    [[nodiscard]] Tensor concat_rows(const Tensor& a, const Tensor& b, const Tensor& c) const;
+
+    // hidden += to_out(attention(LN(hidden) . qkv_weight^T)) in place: the self-attention
+    // half of the reference's UNet::transformer_block (src/cuda/unet.cpp:106-118) with q/k/v
+    // as one projection. hidden fp16 [B, S, 64 heads]; qkv_weight [3W, W] fp16 or packed
+    // E4M3; out_weight [W, W] fp16; out_bias [W].
+    void attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
+                            const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
+                            std::size_t heads) const;
 
 private:
     const Runtime* runtime_ = nullptr;

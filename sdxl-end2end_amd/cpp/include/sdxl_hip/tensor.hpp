@@ -15,7 +15,9 @@
 
 namespace sdxl::hip {
 
-enum class ScalarType : std::uint8_t { Float16, BFloat16, Float32, Int32 };
+// Float8E4M3: finite-only E4M3 codes (bias 7), used for linear weights with an
+// attached per-output-channel dequantisation scale (the reference's FP8 weights).
+enum class ScalarType : std::uint8_t { Float16, BFloat16, Float32, Int32, Float8E4M3 };
 
 [[nodiscard]] std::size_t scalar_size(ScalarType type) noexcept;
 
@@ -30,6 +32,9 @@ struct FloatTensor {
 [[nodiscard]] float half_to_float(std::uint16_t bits) noexcept;
 [[nodiscard]] std::uint16_t float_to_bf16(float value) noexcept;
 [[nodiscard]] float bf16_to_float(std::uint16_t bits) noexcept;
+// E4M3 code -> value (sign, 4-bit exponent bias 7, 3-bit mantissa, subnormals;
+// 0x7F/0xFF are NaN), the reference's decode (src/unet.cpp:91-119).
+[[nodiscard]] float e4m3_to_float(std::uint8_t bits) noexcept;
 
 class Tensor final {
 public:
@@ -51,8 +56,16 @@ public:
     [[nodiscard]] void* data() const noexcept { return data_.get(); }
     [[nodiscard]] const std::int32_t* int32_data() const;
 
+    // Dequantisation scales of an FP8 tensor (fp32, one per output channel or
+    // one for the tensor), as the reference's Tensor::attach_dequant_scale.
+    void attach_dequant_scale(Tensor scale);
+    [[nodiscard]] bool has_dequant_scale() const noexcept { return scale_ != nullptr; }
+    [[nodiscard]] const float* dequant_scale_data() const;
+    [[nodiscard]] std::size_t dequant_scale_count() const noexcept { return scale_ ? scale_->elements() : 0; }
+
 private:
     std::shared_ptr<void> data_;
+    std::shared_ptr<Tensor> scale_;
     std::vector<std::size_t> shape_;
     ScalarType type_ = ScalarType::Float16;
 };

@@ -1,9 +1,11 @@
-// Ops::attention over the C ABI (see ops.hpp). Validation, eligibility errors
-// and the profile label follow the reference's Ops::attention
-// (src/cuda/ops_kernels.cu:1912-1973).
+// Ops over the C ABI (see ops.hpp). Validation, eligibility errors and the
+// profile labels follow the reference's Ops::attention
+// (src/cuda/ops_kernels.cu:1912-1973), Ops::layer_norm (:1428-1460) and
+// Ops::linear (src/cuda/ops_blas.cpp).
 #include "sdxl_hip/ops.hpp"
 
 #include "sdxl_hip/attention.h"
+#include "sdxl_hip/sublayer.h"
 
 #include <sstream>
 
@@ -75,6 +77,152 @@ void Ops::attention_into(const Tensor& query, const Tensor& key, const Tensor& v
                       output.data(), runtime_->stream());
     runtime_->end_profile(scope);
     if (status != SDXL_STATUS_OK) throw HipError(sdxl_last_error());
+}
+
+namespace {
+
+std::size_t rows_of(const Tensor& t) {
+    const std::size_t last = t.shape().back();
+    return last == 0 ? 0 : t.elements() / last;
+}
+
+void check(sdxl_status status) {
+    if (status != SDXL_STATUS_OK) throw HipError(sdxl_last_error());
+}
+
+sdxl_linear_desc linear_desc(const Tensor& input, const Tensor& weight) {
+    if (input.type() != ScalarType::Float16 || input.rank() < 2 || weight.rank() != 2 ||
+        (weight.type() != ScalarType::Float16 && weight.type() != ScalarType::Float8E4M3))
+        throw HipError("linear requires an fp16 input and an fp16 or FP8 E4M3 rank-2 weight");
+    if (weight.size(1) != input.shape().back()) throw HipError("linear feature mismatch");
+    const bool fp8 = weight.type() == ScalarType::Float8E4M3;
+    if (fp8 && (!weight.has_dequant_scale() || weight.dequant_scale_count() != weight.size(0)))
+        throw HipError("FP8 weight has invalid scaling metadata");
+    sdxl_linear_desc d{};
+    d.m = static_cast<std::int64_t>(rows_of(input));
+    d.n = static_cast<std::int64_t>(weight.size(0));
+    d.k = static_cast<std::int64_t>(weight.size(1));
+    d.w_dtype = fp8 ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
+    return d;
+}
+
+void check_bias(const Tensor* bias, std::size_t n) {
+    if (bias != nullptr && (bias->type() != ScalarType::Float16 || bias->rank() != 1 || bias->size(0) != n))
+        throw HipError("linear bias mismatch");
+}
+
+std::string linear_label(const sdxl_linear_desc& d) {
+    std::ostringstream label;
+    label << "ops/linear/" << (d.w_dtype == SDXL_DTYPE_E4M3 ? "e4m3" : "f16") << "/m" << d.m << "_n" << d.n << "_k"
+          << d.k;
+    return label.str();
+}
+
+}  // namespace
+
+Tensor Ops::layer_norm(const Tensor& input, const Tensor& weight, const Tensor& bias, float epsilon) const {
+    if (input.type() != ScalarType::Float16 || weight.type() != ScalarType::Float16 ||
+        bias.type() != ScalarType::Float16 || input.rank() < 2 || weight.rank() != 1 || bias.rank() != 1 ||
+        weight.size(0) != input.shape().back() || bias.size(0) != input.shape().back())
+        throw HipError("CUDA layer norm shape/type mismatch");
+    Tensor output = Tensor::allocate(*runtime_, input.shape(), ScalarType::Float16);
+    const int scope = runtime_->begin_profile("ops/layer_norm/w" + std::to_string(input.shape().back()));
+    const sdxl_status st = sdxl_layer_norm(static_cast<std::int64_t>(rows_of(input)),
+                                           static_cast<std::int64_t>(input.shape().back()), input.data(), 0,
+                                           weight.data(), bias.data(), epsilon, output.data(), 0, runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+    return output;
+}
+
+Tensor Ops::linear(const Tensor& input, const Tensor& weight, const Tensor* bias) const {
+    const sdxl_linear_desc d = linear_desc(input, weight);
+    check_bias(bias, weight.size(0));
+    std::vector<std::size_t> shape = input.shape();
+    shape.back() = weight.size(0);
+    Tensor output = Tensor::allocate(*runtime_, shape, ScalarType::Float16);
+    const int scope = runtime_->begin_profile(linear_label(d));
+    const sdxl_status st =
+        sdxl_linear(&d, input.data(), weight.data(), weight.has_dequant_scale() ? weight.dequant_scale_data() : nullptr,
+                    bias ? bias->data() : nullptr, nullptr, output.data(), runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+    return output;
+}
+
+void Ops::linear_residual_into(const Tensor& input, const Tensor& weight, const Tensor* bias, Tensor& hidden) const {
+    const sdxl_linear_desc d = linear_desc(input, weight);
+    check_bias(bias, weight.size(0));
+    if (hidden.type() != ScalarType::Float16 || hidden.shape().back() != weight.size(0) ||
+        rows_of(hidden) != rows_of(input))
+        throw HipError("linear residual shape mismatch");
+    const int scope = runtime_->begin_profile(linear_label(d) + "_residual");
+    const sdxl_status st =
+        sdxl_linear(&d, input.data(), weight.data(), weight.has_dequant_scale() ? weight.dequant_scale_data() : nullptr,
+                    bias ? bias->data() : nullptr, hidden.data(), hidden.data(), runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+}
+
+Tensor Ops::pack_e4m3(const Tensor& weight) const {
+    if (weight.type() != ScalarType::Float16 || weight.rank() != 2)
+        throw HipError("FP8 weight packing requires an fp16 rank-2 weight");
+    Tensor codes = Tensor::allocate(*runtime_, weight.shape(), ScalarType::Float8E4M3);
+    Tensor scales = Tensor::allocate(*runtime_, {weight.size(0)}, ScalarType::Float32);
+    check(sdxl_quantize_e4m3_rows(static_cast<std::int64_t>(weight.size(0)), static_cast<std::int64_t>(weight.size(1)),
+                                  weight.data(), static_cast<std::uint8_t*>(codes.data()),
+                                  static_cast<float*>(scales.data()), runtime_->stream()));
+    codes.attach_dequant_scale(std::move(scales));
+    return codes;
+}
+
+Tensor Ops::concat_rows(const Tensor& a, const Tensor& b, const Tensor& c) const {
+    for (const Tensor* t : {&a, &b, &c})
+        if (t->rank() != 2 || t->type() != a.type() || t->size(1) != a.size(1))
+            throw HipError("concat_rows requires rank-2 tensors of one type and width");
+    Tensor out = Tensor::allocate(*runtime_, {a.size(0) + b.size(0) + c.size(0), a.size(1)}, a.type());
+    char* dst = static_cast<char*>(out.data());
+    for (const Tensor* t : {&a, &b, &c}) {
+        if (t->bytes() > 0)
+            SDXL_HIP_CHECK(hipMemcpyAsync(dst, t->data(), t->bytes(), hipMemcpyDeviceToDevice, runtime_->stream()));
+        dst += t->bytes();
+    }
+    return out;
+}
+
+void Ops::attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
+                             const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
+                             std::size_t heads) const {
+    if (hidden.type() != ScalarType::Float16 || hidden.rank() != 3 || heads == 0 || hidden.size(2) != heads * 64)
+        throw HipError("attention sublayer requires fp16 hidden [B, S, 64 * heads]");
+    const std::size_t W = hidden.size(2);
+    if (qkv_weight.rank() != 2 || qkv_weight.size(0) != 3 * W || qkv_weight.size(1) != W ||
+        out_weight.type() != ScalarType::Float16 || out_weight.rank() != 2 || out_weight.size(0) != W ||
+        out_weight.size(1) != W || norm_weight.elements() != W || norm_bias.elements() != W ||
+        out_bias.elements() != W)
+        throw HipError("attention sublayer weight mismatch");
+    const bool fp8 = qkv_weight.type() == ScalarType::Float8E4M3;
+    if (fp8 && (!qkv_weight.has_dequant_scale() || qkv_weight.dequant_scale_count() != 3 * W))
+        throw HipError("FP8 weight has invalid scaling metadata");
+    sdxl_sublayer_desc d{};
+    d.batch = static_cast<std::int64_t>(hidden.size(0));
+    d.seq = static_cast<std::int64_t>(hidden.size(1));
+    d.heads = static_cast<std::int64_t>(heads);
+    d.w_qkv_dtype = fp8 ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
+    d.attn_backend = static_cast<std::int32_t>(runtime_->options().attention_backend);
+    const std::size_t ws_bytes = sdxl_attn_sublayer_workspace_bytes(&d);
+    Tensor workspace = Tensor::allocate(*runtime_, {ws_bytes}, ScalarType::Float8E4M3);  // raw bytes
+    std::ostringstream label;
+    label << "unet/attention_sublayer/s" << hidden.size(1) << "_h" << heads << (fp8 ? "_e4m3" : "_f16");
+    const int scope = runtime_->begin_profile(label.str());
+    const sdxl_status st = sdxl_attn_sublayer(
+        &d, hidden.data(), norm_weight.data(), norm_bias.data(), qkv_weight.data(),
+        fp8 ? qkv_weight.dequant_scale_data() : nullptr, out_weight.data(), out_bias.data(), hidden.data(),
+        workspace.data(), ws_bytes, runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+    // The workspace is released when `workspace` goes out of scope; hipFree
+    // waits for the work queued on it.
 }
 
 }  // namespace sdxl::hip

@@ -2,6 +2,8 @@
 #include "sdxl_hip/tensor.hpp"
 
 #include <bit>
+#include <cmath>
+#include <limits>
 #include <cstring>
 #include <functional>
 #include <numeric>
@@ -14,8 +16,29 @@ std::size_t scalar_size(ScalarType type) noexcept {
     case ScalarType::BFloat16: return 2;
     case ScalarType::Float32:
     case ScalarType::Int32: return 4;
+    case ScalarType::Float8E4M3: return 1;
     }
     return 0;
+}
+
+float e4m3_to_float(std::uint8_t bits) noexcept {
+    const std::uint32_t exponent = (bits >> 3) & 0xFU, mantissa = bits & 0x7U;
+    float value;
+    if ((bits & 0x7FU) == 0x7FU) value = std::numeric_limits<float>::quiet_NaN();
+    else if (exponent == 0) value = std::ldexp(static_cast<float>(mantissa) / 8.0F, -6);
+    else value = std::ldexp(1.0F + static_cast<float>(mantissa) / 8.0F, static_cast<int>(exponent) - 7);
+    return (bits & 0x80U) ? -value : value;
+}
+
+void Tensor::attach_dequant_scale(Tensor scale) {
+    if (scale.type() != ScalarType::Float32 || scale.rank() != 1)
+        throw HipError("FP8 weight has invalid scaling metadata");
+    scale_ = std::make_shared<Tensor>(std::move(scale));
+}
+
+const float* Tensor::dequant_scale_data() const {
+    if (!scale_) throw HipError("FP8 weight has invalid scaling metadata");
+    return static_cast<const float*>(scale_->data());
 }
 
 // binary32 -> binary16, round to nearest even; overflow to infinity, NaN kept quiet.
@@ -110,6 +133,7 @@ Tensor Tensor::from_host_f32(const Runtime& runtime, const FloatTensor& host, Sc
         return t;
     }
     if (type == ScalarType::Int32) throw HipError("use from_host_i32 for int32 tensors");
+    if (type == ScalarType::Float8E4M3) throw HipError("use Ops::pack_e4m3 for FP8 weights");
     std::vector<std::uint16_t> bits(host.values.size());
     for (std::size_t i = 0; i < bits.size(); ++i)
         bits[i] = type == ScalarType::Float16 ? float_to_half(host.values[i]) : float_to_bf16(host.values[i]);
@@ -136,6 +160,13 @@ FloatTensor Tensor::to_host_f32(const Runtime& runtime) const {
     if (type_ == ScalarType::Float32) {
         SDXL_HIP_CHECK(hipMemcpyAsync(host.values.data(), data(), bytes(), hipMemcpyDeviceToHost, runtime.stream()));
         runtime.synchronize();
+        return host;
+    }
+    if (type_ == ScalarType::Float8E4M3) {
+        std::vector<std::uint8_t> codes(elements());
+        SDXL_HIP_CHECK(hipMemcpyAsync(codes.data(), data(), bytes(), hipMemcpyDeviceToHost, runtime.stream()));
+        runtime.synchronize();
+        for (std::size_t i = 0; i < codes.size(); ++i) host.values[i] = e4m3_to_float(codes[i]);
         return host;
     }
     if (type_ == ScalarType::Int32) {

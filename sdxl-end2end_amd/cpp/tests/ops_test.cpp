@@ -57,6 +57,9 @@ void host_cases() {
     require(float_to_half(65520.0F) == 0x7C00 && float_to_half(1.0F + 1.0F / 2048.0F) == 0x3C00, "half rounding");
     require(half_to_float(0x0001) == std::ldexp(1.0F, -24), "half subnormal");
     require(float_to_bf16(1.0F) == 0x3F80 && bf16_to_float(0x3F80) == 1.0F, "bf16");
+    // E4M3 decode (src/unet.cpp:91-119): 1.0, max 448, smallest subnormal 2^-9, NaN code
+    require(e4m3_to_float(0x38) == 1.0F && e4m3_to_float(0x7E) == 448.0F && e4m3_to_float(0xFE) == -448.0F, "e4m3");
+    require(e4m3_to_float(0x01) == std::ldexp(1.0F, -9) && std::isnan(e4m3_to_float(0x7F)), "e4m3 edges");
     std::cout << "host cases passed\n";
 }
 
@@ -68,6 +71,99 @@ FloatTensor filled(std::vector<std::size_t> shape, const std::function<float(std
     t.values.resize(n);
     for (std::size_t i = 0; i < n; ++i) t.values[i] = f(i);
     return t;
+}
+
+// Host fp32 references of the sublayer operators (src/unet.cpp:202-263).
+std::vector<float> host_layer_norm(const FloatTensor& x, std::size_t W) {
+    std::vector<float> y(x.values.size());
+    for (std::size_t r = 0; r < x.values.size() / W; ++r) {
+        const float* s = x.values.data() + r * W;
+        float mean = 0.0F, var = 0.0F;
+        for (std::size_t i = 0; i < W; ++i) mean += s[i];
+        mean /= static_cast<float>(W);
+        for (std::size_t i = 0; i < W; ++i) var += (s[i] - mean) * (s[i] - mean);
+        const float inv = 1.0F / std::sqrt(var / static_cast<float>(W) + 1.0e-5F);
+        for (std::size_t i = 0; i < W; ++i) y[r * W + i] = (s[i] - mean) * inv;
+    }
+    return y;
+}
+
+std::vector<float> host_linear(const std::vector<float>& x, const std::vector<float>& w, std::size_t rows,
+                               std::size_t n, std::size_t k) {
+    std::vector<float> y(rows * n, 0.0F);
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t o = 0; o < n; ++o) {
+            float acc = 0.0F;
+            for (std::size_t i = 0; i < k; ++i) acc += x[r * k + i] * w[o * k + i];
+            y[r * n + o] = acc;
+        }
+    return y;
+}
+
+void sublayer_cases() {
+    Runtime runtime;
+    Ops ops(runtime);
+    const std::size_t rows = 96, W = 128, N = 192;
+    const auto x = filled({2, rows / 2, W}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.37F) * 2.0F; });
+    const auto ones = filled({W}, [](std::size_t) { return 1.0F; });
+    const auto zeros = filled({W}, [](std::size_t) { return 0.0F; });
+    auto xd = Tensor::from_host_f32(runtime, x);
+    const auto ln = ops.layer_norm(xd, Tensor::from_host_f32(runtime, ones), Tensor::from_host_f32(runtime, zeros))
+                        .to_host_f32(runtime);
+    const auto ln_ref = host_layer_norm(x, W);
+    for (std::size_t i = 0; i < ln_ref.size(); ++i)
+        require_close(ln.values[i], ln_ref[i], std::fabs(ln_ref[i]) * 1e-3F + 1e-4F, "layer_norm");
+
+    const auto w = filled({N, W}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.11F) * 0.05F; });
+    auto wd = Tensor::from_host_f32(runtime, w);
+    const auto lin = ops.linear(xd, wd).to_host_f32(runtime);
+    const auto lin_ref = host_linear(x.values, Tensor::from_host_f32(runtime, w).to_host_f32(runtime).values, rows, N, W);
+    for (std::size_t i = 0; i < lin_ref.size(); ++i)
+        require_close(lin.values[i], lin_ref[i], std::fabs(lin_ref[i]) * 1e-3F + 1e-3F, "linear fp16");
+
+    const auto packed = ops.pack_e4m3(wd);
+    require(packed.type() == ScalarType::Float8E4M3 && packed.dequant_scale_count() == N, "pack_e4m3");
+    auto scales = std::vector<float>(N);
+    SDXL_HIP_CHECK(hipMemcpy(scales.data(), packed.dequant_scale_data(), N * 4, hipMemcpyDeviceToHost));
+    auto deq = packed.to_host_f32(runtime).values;
+    for (std::size_t o = 0; o < N; ++o)
+        for (std::size_t i = 0; i < W; ++i) deq[o * W + i] *= scales[o];
+    const auto lin8 = ops.linear(xd, packed).to_host_f32(runtime);
+    const auto lin8_ref = host_linear(x.values, deq, rows, N, W);
+    for (std::size_t i = 0; i < lin8_ref.size(); ++i)
+        require_close(lin8.values[i], lin8_ref[i], std::fabs(lin8_ref[i]) * 1e-3F + 1e-3F, "linear e4m3");
+    require_throws([&] { (void)ops.linear(xd, Tensor::from_host_f32(runtime, filled({N, 64}, [](std::size_t) { return 0.0F; }))); },
+                   "linear feature mismatch", "linear shape");
+    require_throws([&] { (void)ops.layer_norm(xd, wd, wd); }, "CUDA layer norm shape/type mismatch", "layer_norm shape");
+
+    // attention_sublayer == layer_norm -> linear(qkv) -> attention -> linear_residual_into
+    const std::size_t heads = 2;
+    const auto wq = filled({3 * W, W}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.013F) * 0.06F; });
+    const auto wo = filled({W, W}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.029F) * 0.06F; });
+    const auto bo = filled({W}, [](std::size_t i) { return 0.01F * static_cast<float>(i % 7); });
+    const auto qkv8 = ops.pack_e4m3(Tensor::from_host_f32(runtime, wq));
+    auto wod = Tensor::from_host_f32(runtime, wo);
+    auto bod = Tensor::from_host_f32(runtime, bo);
+    auto gd = Tensor::from_host_f32(runtime, ones);
+    auto bd = Tensor::from_host_f32(runtime, zeros);
+    auto fused = Tensor::from_host_f32(runtime, x);
+    ops.attention_sublayer(fused, gd, bd, qkv8, wod, bod, heads);
+    auto step = Tensor::from_host_f32(runtime, x);
+    const auto n = ops.layer_norm(step, gd, bd);
+    const auto qkv = ops.linear(n, qkv8).to_host_f32(runtime);  // [2, 48, 3W] on the host, split below
+    FloatTensor qh{{2, rows / 2, W}, {}}, kh{{2, rows / 2, W}, {}}, vh{{2, rows / 2, W}, {}};
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t c = 0; c < W; ++c) {
+            qh.values.push_back(qkv.values[r * 3 * W + c]);
+            kh.values.push_back(qkv.values[r * 3 * W + W + c]);
+            vh.values.push_back(qkv.values[r * 3 * W + 2 * W + c]);
+        }
+    const auto attn = ops.attention(Tensor::from_host_f32(runtime, qh), Tensor::from_host_f32(runtime, kh),
+                                    Tensor::from_host_f32(runtime, vh), heads);
+    ops.linear_residual_into(attn, wod, &bod, step);
+    const auto a = fused.to_host_f32(runtime).values, b = step.to_host_f32(runtime).values;
+    for (std::size_t i = 0; i < a.size(); ++i) require(a[i] == b[i], "attention_sublayer == composition");
+    std::cout << "sublayer cases passed\n";
 }
 
 void device_cases() {
@@ -144,6 +240,7 @@ void device_cases() {
     for (float x : cudnn_ops.attention(q2, q2, v2, 1).to_host_f32(cudnn_runtime).values)
         require_close(x, 3.0F, 0.02F, "cudnn-sdpa spelling runs the fused kernel");
     std::cout << "device cases passed\n";
+    sublayer_cases();
 }
 
 }  // namespace

@@ -1,4 +1,5 @@
-"""The C++20 host API (sdxl-end2end_amd/cpp): Runtime / Tensor / Ops::attention over the C ABI.
+"""The C++20 host API (sdxl-end2end_amd/cpp): Runtime / Tensor / Ops (attention, layer_norm, linear,
+E4M3 packing, attention_sublayer) over the C ABI.
 
 Runs the CTest-style executable like the reference runs tests/cuda/cuda_ops_test.cu:
 host-only cases here, every case on the GPU box.
@@ -30,6 +31,7 @@ def test_device_cases():
     r = _run("sdxl_hip_ops_test")
     assert r.returncode == 0, r.stdout + r.stderr
     assert "device cases passed" in r.stdout
+    assert "sublayer cases passed" in r.stdout
 
 
 @pytest.mark.gpu
