@@ -165,31 +165,49 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
 
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
 
-template <int kWaves, bool IsBf16, bool kMaskAll>
-__global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(FusedAttentionParams p) {
+// The kernel body for one workgroup kind (kSplit: key-split workgroup).
+template <int kWaves, bool IsBf16, bool kMaskAll, bool kSplit>
+__device__ __attribute__((always_inline)) inline void attention_body(const FusedAttentionParams& p,
+                                                                     char (*ring)[kTileBytes]) {
     constexpr int kBlockQueries = kWaves * 32;
     constexpr int kLoadsPerWave = 16 / kWaves;  // 1-KiB transfers per wave and tile (K and V)
-    __shared__ __attribute__((aligned(16))) char kring[kKRing][kTileBytes];
-    __shared__ __attribute__((aligned(16))) char vring[kVRing][kTileBytes];
+    char (*kring)[kTileBytes] = ring;
+    char (*vring)[kTileBytes] = ring + kKRing;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hf = lane >> 5;   // which half of the wave
     const int col = lane & 31;  // query column of this lane in the 32x32 tiles
 
-    // XCD-aware task order: the hardware deals workgroup ids round robin over
-    // the 8 XCDs, so give each XCD one contiguous range of tasks (consecutive
-    // query blocks of the same head share K/V in that XCD's L2).
+    // Workgroup kinds. Whole: 128 query rows (4 waves x 32), all keys.
+    // Key-split (ids >= whole_units): 64 query rows; wave w takes rows
+    // 32 (w & 1) .. +31 and key half w >> 1, and the two halves of each row
+    // block are merged through LDS at the end. Mixing the kinds lets a call
+    // fill every resident workgroup slot with equal work (see the launcher).
+    // XCD-aware order within each kind: the hardware deals workgroup ids round
+    // robin over the 8 XCDs, so each XCD gets one contiguous range of tasks
+    // (row blocks of the same head share K/V in that XCD's L2).
+    constexpr bool split = kSplit;
     int task;
     {
-        const int n = p.total_blocks;
-        const int id = blockIdx.x;
+        const int n = split ? p.split_units : p.whole_units;
+        const int id = split ? (int)blockIdx.x - p.whole_units : (int)blockIdx.x;
         const int xcd = id & 7, slot = id >> 3;
         const int per = n >> 3, extra = n & 7;
         task = xcd * per + (xcd < extra ? xcd : extra) + slot;
     }
-    const int qblk = task % p.q_blocks;
-    const int bh = task / p.q_blocks;
+    const int khalf = split ? wave >> 1 : 0;  // key half of a key-split wave
+    int bh, q0;
+    if (!split) {
+        bh = task / p.q_blocks;
+        q0 = (task % p.q_blocks) * kBlockQueries + wave * 32;
+    } else {
+        const int blocks64 = p.q_seq / 64;  // q_seq % 128 == 0 for key-split calls
+        const int gb = 2 * p.whole_units + task;
+        bh = gb / blocks64;
+        q0 = (gb % blocks64) * 64 + (wave & 1) * 32;
+    }
+    const int qblk = q0 / kBlockQueries;
     const int h = bh % p.heads;
     const int b = bh / p.heads;
 
@@ -200,7 +218,6 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     char* obase = (char*)p.o + ((int64_t)b * p.q_seq * p.o_row_stride + (int64_t)h * kHeadDim) * elem;
     const int64_t ks_bytes = p.k_row_stride * elem, vs_bytes = p.v_row_stride * elem;
 
-    const int q0 = qblk * kBlockQueries + wave * 32;
     const int my_query = q0 + col;
 
     const float c = p.scale_log2;
@@ -222,7 +239,10 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         const int last_query = qblk * kBlockQueries + kBlockQueries - 1;
         n_keys = n_keys < last_query + 1 ? n_keys : last_query + 1;
     }
-    const int n_tiles = (n_keys + kKeyTile - 1) / kKeyTile;
+    // Key-split calls: stage t holds keys 32t .. +31 of each half (rows 0-31
+    // half 0, rows 32-63 half 1); k_seq % 64 == 0.
+    const int half_keys = p.k_seq / 2;
+    const int n_tiles = split ? p.k_seq / kKeyTile : (n_keys + kKeyTile - 1) / kKeyTile;
     // Tiles [0, n_plain) are complete and need no mask (kMaskAll covers key-mask
     // and causal calls, where every tile is masked).
     const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
@@ -248,6 +268,26 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
             const int row = 8 * (n & 7) + (lane >> 3);
             const int key = min(row, p.k_seq - 1 - key0);  // clamp rows of a partial tile
             const uint32_t off = __umul24((uint32_t)key, (uint32_t)stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
+            lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
+        }
+    };
+
+    // Key-split stages: transfer n covers 8 rows of one key half (rows 0-31
+    // half 0, 32-63 half 1); stage t holds keys 32t .. +31 of each half.
+    auto issue_split = [&](int kt, int vt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < kLoadsPerWave; ++j) {
+            const int n = wave * kLoadsPerWave + j;
+            const bool is_v = n >= 8;
+            const int tile = is_v ? vt : kt;
+            if (tile < 0 || tile >= n_tiles) continue;
+            const int half = (n & 7) >> 2;
+            const int64_t stride = is_v ? vs_bytes : ks_bytes;
+            const char* tile_base = (is_v ? vbase : kbase) + (int64_t)(half * half_keys + 32 * tile) * stride;
+            const int row = 8 * (n & 7) + (lane >> 3);
+            const uint32_t off = __umul24((uint32_t)(row - 32 * half), (uint32_t)stride) +
+                                 (uint32_t)(((lane & 7) ^ swz(row)) << 4);
             const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
             lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
         }
@@ -346,7 +386,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     // the group after next (tile buffer kn2, group g2) are prefetched into kop.
     // kMasked/kExact: exact maximum over the whole group first (masked tiles,
     // first tile); otherwise each half is checked for overflow after the fact.
-    auto group_step = [&]<bool kMasked, bool kExact>(f32x16& s_cur, f32x16& s_next, i16x8 (&kop)[4], const char* vb,
+    auto group_step = [&]<bool kMasked, bool kExact, bool kPrefetchK = true>(f32x16& s_cur, f32x16& s_next, i16x8 (&kop)[4], const char* vb,
                                                      int g, int t, uint64_t vis, const char* kn2, int g2,
                                                      bool have_next) __attribute__((always_inline)) {
         i16x8 vop[2];
@@ -421,7 +461,7 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
 #pragma unroll
         for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
-        load_k(kn2, g2, kop);
+        if constexpr (kPrefetchK) load_k(kn2, g2, kop);
         __builtin_amdgcn_sched_barrier(0);
         // 6: PV half 0, d 32-63 | pack + row sum of half 1, overflow check
         acc[1] = mfma32<IsBf16>(vop[1], p0, acc[1]);
@@ -459,6 +499,63 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     // and two V buffers suffice. sa/sb: scores of groups 0/1.
     f32x16 sa, sb;
     i16x8 kop[4];
+    if constexpr (split) {
+        // ---- key-split workgroup: one 32-key group per stage and wave (group
+        // khalf of the stage buffers). The group after next lies in a stage not
+        // yet resident, so each stage loads the next group's K operands at its
+        // start instead of prefetching them a step earlier.
+        issue_split(0, 0);
+        issue_split(1, -1);
+        wait_vmem_all();
+        __syncthreads();
+        load_k(kring[0], khalf, kop);
+        sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+        auto stage = [&]<bool kFirst, bool kOdd>(int t) __attribute__((always_inline)) {
+            wait_vmem_all();  // this lane's transfers of K(t+1), V(t) landed
+            __syncthreads();  // ... and every lane's; stage t-1 fully consumed
+            issue_split(t + 2, t + 1);
+            load_k(kring[kOdd ? 0 : 1], khalf, kop);  // K(t+1) (stale past the end, unused)
+            const char* v_t = vring[kOdd ? 1 : 0];
+            if constexpr (kOdd) group_step.template operator()<false, kFirst, false>(sb, sa, kop, v_t, khalf, t, ~0ull, v_t, 0, true);
+            else group_step.template operator()<false, kFirst, false>(sa, sb, kop, v_t, khalf, t, ~0ull, v_t, 0, true);
+        };
+        int t = 0;
+        if (n_tiles > 0) {
+            stage.template operator()<true, false>(0);
+            for (t = 1; t + 1 < n_tiles; t += 2) {
+                stage.template operator()<false, true>(t);
+                stage.template operator()<false, false>(t + 1);
+            }
+            if (t < n_tiles) stage.template operator()<false, true>(t);
+        }
+        // ---- merge the key halves: half-1 waves park (O, anchor, row sum) in
+        // LDS, half-0 waves combine in fixed order and store.
+        __syncthreads();  // every wave is done with the stage buffers
+        float* park = (float*)&ring[0][0] + (wave & 1) * (34 * 64) + lane;
+        if (khalf == 1) {
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) park[(16 * dt + i) * 64] = acc[dt][i];
+            park[32 * 64] = anchored ? m_run : -__builtin_inff();
+            park[33 * 64] = l_run;
+        }
+        __syncthreads();
+        if (khalf == 1) return;
+        const float m0 = anchored ? m_run : -__builtin_inff();
+        const float m1 = park[32 * 64];
+        const float mx = fmaxf(m0, m1);
+        // Scale factors 2^(m - mx); an empty half (-inf) weighs 0.
+        const float a0 = m0 == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m0 - mx);
+        const float a1 = m1 == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m1 - mx);
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[dt][i] = acc[dt][i] * a0 + park[(16 * dt + i) * 64] * a1;
+        l_run = l_run * a0 + park[33 * 64] * a1;
+    } else {
     if (n_tiles > 0) {
         issue(0, 0);
         issue(1, -1);
@@ -513,6 +610,8 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         if (t + 1 < n_tiles) tile.template operator()<true, false, true>(t + 1);
     }
 
+    }  // whole workgroup
+
     // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
     // dims 32dt + 8u + 4hf + (0..3) of its query in acc[dt][4u .. 4u+3].
     const float l_tot = xhalf_sum(l_run);
@@ -531,18 +630,57 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     }
 }
 
+// Whole and key-split workgroups share one kernel (one grid); each kind is
+// a separate instantiation of the body, so neither constrains the other's
+// register allocation. K ring then V ring in one array (the key-split merge
+// reuses all of it).
+template <int kWaves, bool IsBf16, bool kMaskAll>
+__global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(FusedAttentionParams p) {
+    __shared__ __attribute__((aligned(16))) char ring[kKRing + kVRing][kTileBytes];
+    if constexpr (!kMaskAll) {
+        if ((int)blockIdx.x >= p.whole_units) {
+            attention_body<kWaves, IsBf16, false, true>(p, ring);
+            return;
+        }
+    }
+    attention_body<kWaves, IsBf16, kMaskAll, false>(p, ring);
+}
+
 }  // namespace
 
 int fused_attention_block_queries() { return 32 * kFusedWaves; }
 
-hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, bool is_bf16, hipStream_t stream) {
+hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, bool is_bf16, int compute_units,
+                                      hipStream_t stream) {
     FusedAttentionParams p = params_in;
     constexpr int kBlockQueries = 32 * kFusedWaves;
     p.q_blocks = (p.q_seq + kBlockQueries - 1) / kBlockQueries;
     p.total_blocks = p.q_blocks * p.heads * p.batch;
     if (p.total_blocks == 0) return hipSuccess;
+    // Work split. Three workgroups are resident per CU (occupancy 3, one wave
+    // per SIMD each). When the 128-row units leave slots idle (U < S), part of
+    // them is replaced by key-split workgroups (64 rows, each wave half the
+    // keys: half the work of a whole workgroup) so that the grid is exactly S
+    // workgroups, 2U - S whole and 2S - 2U split (at U < S/2: 2U split ones).
+    // The hardware deals ids x, x + CUs, x + 2 CUs to one CU, so with whole
+    // workgroups first every CU gets the same mix. Non-causal, unmasked calls
+    // with q_seq % 128 == 0 and k_seq % 64 == 0 only.
+    p.whole_units = p.total_blocks;
+    p.split_units = 0;
+    const int64_t slots = (int64_t)compute_units * 3;
+    const int64_t units = p.total_blocks;
+    if (compute_units > 0 && !p.causal && p.key_mask == nullptr && p.q_seq % 128 == 0 && p.k_seq % 64 == 0 &&
+        p.k_seq > 0 && units < slots) {
+        if (2 * units >= slots) {
+            p.whole_units = (int32_t)(2 * units - slots);
+            p.split_units = (int32_t)(2 * slots - 2 * units);
+        } else {
+            p.whole_units = 0;
+            p.split_units = (int32_t)(2 * units);
+        }
+    }
     const bool mask_all = p.causal || p.key_mask != nullptr;
-    const dim3 grid(p.total_blocks), block(64 * kFusedWaves);
+    const dim3 grid(p.whole_units + p.split_units), block(64 * kFusedWaves);
     if (is_bf16) {
         if (mask_all) hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, false>), grid, block, 0, stream, p);

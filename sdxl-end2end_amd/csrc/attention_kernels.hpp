@@ -27,10 +27,14 @@ struct FusedAttentionParams {
     int32_t q_blocks;      // filled by the launcher
     int32_t total_blocks;  // filled by the launcher
     float scale_log2;      // softmax scale * log2(e)
+    int32_t whole_units;   // filled by the launcher: 128-row workgroups (ids first)
+    int32_t split_units;   // filled by the launcher: 64-row key-split workgroups
 };
 
 // head_dim 64, fp16 or bf16 storage, 16-byte aligned rows.
-hipError_t launch_fused_attention_d64(const FusedAttentionParams& params, bool is_bf16, hipStream_t stream);
+// compute_units: CUs of the device (0 if unknown; disables key-split workgroups).
+hipError_t launch_fused_attention_d64(const FusedAttentionParams& params, bool is_bf16, int compute_units,
+                                      hipStream_t stream);
 int fused_attention_block_queries();
 
 struct OnlineAttentionParams {

@@ -34,6 +34,19 @@ int64_t eff_stride(int64_t stride, int64_t width) { return stride == 0 ? width :
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
+// CUs of the current device, cached per device (0 if unknown).
+int compute_units() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
+        cached[dev] = cus > 0 ? cus : -1;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
 // Checks everything sdxl_attn_fwd checks that does not involve pointers.
 sdxl_status validate_desc(const sdxl_attn_desc* d) {
     if (d == nullptr) return fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn: null descriptor");
@@ -210,7 +223,7 @@ sdxl_status sdxl_attn_fwd(const sdxl_attn_desc* d, const void* q, const void* k,
         const int64_t blocks = ((d->q_seq + sdxl_hip::fused_attention_block_queries() - 1) /
                                 sdxl_hip::fused_attention_block_queries()) * d->heads * d->batch;
         if (blocks > INT32_MAX) return fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_attn: grid too large");
-        err = sdxl_hip::launch_fused_attention_d64(p, d->dtype == SDXL_DTYPE_BF16, s);
+        err = sdxl_hip::launch_fused_attention_d64(p, d->dtype == SDXL_DTYPE_BF16, compute_units(), s);
     }
     if (err != hipSuccess)
         return fail(SDXL_STATUS_LAUNCH_FAILED, std::string("sdxl_attn launch: ") + hipGetErrorString(err));
