@@ -658,25 +658,27 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     p.total_blocks = p.q_blocks * p.heads * p.batch;
     if (p.total_blocks == 0) return hipSuccess;
     // Work split. Three workgroups are resident per CU (occupancy 3, one wave
-    // per SIMD each). When the 128-row units leave slots idle (U < S), part of
-    // them is replaced by key-split workgroups (64 rows, each wave half the
-    // keys: half the work of a whole workgroup) so that the grid is exactly S
-    // workgroups, 2U - S whole and 2S - 2U split (at U < S/2: 2U split ones).
+    // per SIMD each), S = 3 CUs slots. With U 128-row units, the rounds that
+    // fill every slot run whole workgroups; the remaining R = U mod S units are
+    // re-cut so that the last round is full too: part of them becomes
+    // key-split workgroups (64 rows, each wave half the keys: half the work of
+    // a whole one), 2R - S whole and 2S - 2R split (at R < S/2: 2R split).
     // The hardware deals ids x, x + CUs, x + 2 CUs to one CU, so with whole
-    // workgroups first every CU gets the same mix. Non-causal, unmasked calls
-    // with q_seq % 128 == 0 and k_seq % 64 == 0 only.
+    // workgroups first every CU of the last round gets the same mix.
+    // Non-causal, unmasked calls with q_seq % 128 == 0 and k_seq % 64 == 0.
     p.whole_units = p.total_blocks;
     p.split_units = 0;
     const int64_t slots = (int64_t)compute_units * 3;
     const int64_t units = p.total_blocks;
     if (compute_units > 0 && !p.causal && p.key_mask == nullptr && p.q_seq % 128 == 0 && p.k_seq % 64 == 0 &&
-        p.k_seq > 0 && units < slots) {
-        if (2 * units >= slots) {
-            p.whole_units = (int32_t)(2 * units - slots);
-            p.split_units = (int32_t)(2 * slots - 2 * units);
+        p.k_seq > 0 && units % slots != 0) {
+        const int64_t full = units - units % slots, rem = units % slots;
+        if (2 * rem >= slots) {
+            p.whole_units = (int32_t)(full + 2 * rem - slots);
+            p.split_units = (int32_t)(2 * slots - 2 * rem);
         } else {
-            p.whole_units = 0;
-            p.split_units = (int32_t)(2 * units);
+            p.whole_units = (int32_t)full;
+            p.split_units = (int32_t)(2 * rem);
         }
     }
     const bool mask_all = p.causal || p.key_mask != nullptr;

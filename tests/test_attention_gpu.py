@@ -291,3 +291,30 @@ def test_hip_graph_capture_replays():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), i
         _ = (q.float() * 2).sum().item()  # unrelated eager work between replays
+
+
+# ---------------------------------------------------------------- key-split workgroups
+# Unmasked, non-causal calls with Sq % 128 == 0 and Sk % 64 == 0 fill the device's resident
+# workgroup slots with a mix of whole (128 rows, all keys) and key-split (64 rows, two waves per
+# row block on half the keys each, merged through LDS) workgroups. These shapes run all-split,
+# mixed, and mixed in a second round on an MI355X (256 CUs, 768 slots).
+
+@pytest.mark.parametrize("B,Sq,Sk,H", [
+    (1, 128, 64, 1),      # one stage: each key half is 32 keys
+    (1, 256, 512, 2),     # 4 units -> 8 key-split workgroups
+    (2, 384, 1088, 3),    # 18 units, Sk not a multiple of 128
+    (1, 3584, 512, 60),   # 1680 units: two full rounds of whole workgroups, then a mixed round
+])
+def test_key_split_workgroups(B, Sq, Sk, H):
+    qb, kb, vb = seeded(880 + Sq, B, Sq, H * 64), seeded(881 + Sk, B, Sk, H * 64), seeded(882, B, Sk, H * 64)
+    got = run(qb, kb, vb, H)
+    if B * H * Sq * Sk <= 4096 * 4096:
+        ref = oracle.attention_f16(qb, kb, vb, H, threads=THREADS)
+        assert_parity(got, ref, label=f"split B{B} Sq{Sq} Sk{Sk} H{H}")
+    else:
+        for r0, r1 in [(0, 40), (Sq // 2, Sq // 2 + 40), (Sq - 40, Sq)]:
+            ref = oracle.attention_f16_rows(qb, kb, vb, H, r0, r1)
+            assert_parity(got[:, r0:r1], ref[:, r0:r1], label=f"split rows {r0}:{r1}")
+        tref = torch_reference(qb, kb, vb, H)
+        assert_parity(got, tref, label="split torch")
+    assert (run(qb, kb, vb, H) == got).all()
