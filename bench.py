@@ -7,8 +7,8 @@ self-attention, fp16 Q,K,V [2, 10, 4096, 64] (configs[2]; BSHD storage
 
 One "step" = one sdxl_attn_fwd call over the whole [2, 10, 4096, 4096] problem,
 inputs resident in HBM. Timing: W untimed warm-up calls, then K calls bracketed
-by torch.cuda.synchronize(); per-launch HIP events on the launch stream give
-the kernel's average duration for the roofline figure.
+by torch.cuda.synchronize(); a HIP event pair on the launch stream around the same
+K launches gives the average launch duration for the roofline figure.
 
 Also printed (same JSON line): the roofline object, the CPU baseline (the
 reference's own full_attention, compiled from its sources into
@@ -40,6 +40,9 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...) and exit")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="profiling aid: power-limited ceilings (hipBLASLt fp16 GEMM and the c3 attention on "
+                         "random vs zero operands) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -56,23 +59,29 @@ def make_inputs(torch, B, Sq, Sk, H, seed):
 
 
 def time_calls(torch, sh, q, k, v, heads, steps, warmup):
-    """Returns (ms per step over the timed region, mean kernel ms from per-launch events)."""
+    """Returns (ms per step over the timed region, mean launch ms from HIP events, output).
+
+    The timed region is `steps` back-to-back calls bracketed by torch.cuda.synchronize(); one
+    HIP event pair on the launch stream (the current stream, which sdxl_hip.attention launches
+    on) brackets the same launches, so the mean launch duration is (end - start) / steps and
+    includes the dispatch gaps between launches. No per-launch events: recording them between
+    launches inserts gaps of their own."""
     out = torch.empty_like(q)
     for _ in range(warmup):
         sh.attention(q, k, v, heads, out=out)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
+    start.record(stream)
+    for _ in range(steps):
         sh.attention(q, k, v, heads, out=out)
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    kernel_ms = sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / steps
+    kernel_ms = start.elapsed_time(end) / steps
     return wall_ms, kernel_ms, out
 
 
@@ -153,6 +162,31 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
     return out
 
 
+def ceiling(torch, sh):
+    """Data-dependent throughput: the same instruction streams on N(0,1) operands and on a zero
+    operand. MFMA power scales with operand toggling; on random data the device lowers its clock."""
+    res = {}
+    n = 8192
+    a = torch.randn(n, n, device="cuda:0", dtype=torch.float16)
+    b = torch.randn(n, n, device="cuda:0", dtype=torch.float16)
+    for label in ("randn", "zero_b"):
+        if label == "zero_b":
+            b.zero_()
+        ms = time_fn(torch, lambda: torch.matmul(a, b), 10, 3, reps=5)
+        res[f"hipblaslt_gemm_{n}_{label}_tflops"] = round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)
+    del a, b
+    B, Sq, Sk, H = 2, 4096, 4096, 10
+    q, k, v = make_inputs(torch, B, Sq, Sk, H, 1234)
+    o = torch.empty_like(q)
+    for label in ("randn", "zero_q"):
+        if label == "zero_q":
+            q.zero_()
+        ms = time_fn(torch, lambda: sh.attention(q, k, v, H, out=o), 30, 3)
+        res[f"attention_c3_{label}_us"] = round(ms * 1e3, 2)
+        res[f"attention_c3_{label}_tflops"] = round(sh.attention_flops(B, H, Sq, Sk) / (ms * 1e-3) / 1e12, 1)
+    return res
+
+
 def read_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 --pmc summary."""
     try:
@@ -225,6 +259,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         return
+    if args.ceiling:
+        print(json.dumps(ceiling(torch, sh)), flush=True)
+        return
     if args.only == "c4":
         print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
@@ -274,11 +311,14 @@ def main():
             if name == "c3":
                 continue
             qq, kk, vv = make_inputs(torch, b, sq, sk, h, 99)
-            w_ms, k_ms, _ = time_calls(torch, sh, qq, kk, vv, h, 100, 10)
+            w_ms, _, oo = time_calls(torch, sh, qq, kk, vv, h, 100, 10)
+            # device time per call from captured-graph replays: the per-launch host cost of the
+            # ctypes call (~6 us) would otherwise dominate these short kernels
+            k_ms = time_fn(torch, lambda: sh.attention(qq, kk, vv, h, out=oo), 20, 2)
             fl = sh.attention_flops(b, h, sq, sk)
             by = sh.attention_bytes(b, h, sq, sk)
             sec[name] = {"shape": [b, h, sq, sk, 64], "what": label, "us_per_call": round(w_ms * 1e3, 2),
-                         "kernel_us": round(k_ms * 1e3, 2), "tflops": round(fl / (k_ms * 1e-3) / 1e12, 1),
+                         "kernel_us": round(k_ms * 1e3, 2), "kernel_timing": "HIP graph replay", "tflops": round(fl / (k_ms * 1e-3) / 1e12, 1),
                          "mfma_frac": round(fl / (k_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
                          "hbm_gbs": round(by / (k_ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}

@@ -64,6 +64,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
 typedef __attribute__((address_space(3))) char lds_char;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 
 constexpr int kHeadDim = 64;
 constexpr int kKeyTile = 64;
@@ -646,6 +649,256 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
     attention_body<kWaves, IsBf16, kMaskAll, false>(p, ring);
 }
 
+// ---- short key sequences (k_seq <= 128: the 77-token cross-attention, CLIP).
+// One workgroup owns a chunk of consecutive 32-row query blocks of one
+// (batch, head): it stages that head's whole K and V (at most 128 rows each)
+// in LDS once, then each wave walks its blocks (w, w + kWaves, ...) computing
+// the exact softmax in one pass (no running anchor, no rescaling):
+// S^T = K Q^T for all key groups, one maximum, exp2, one sum, O^T = V^T P^T.
+// The Q operands of a wave's next block are loaded before the current block
+// is computed, so HBM reads overlap the matrix/VALU work and the stores.
+// The VALU work per block is kept small (about one wave per SIMD leaves no
+// latency hiding): Q is used as stored and the scale is folded into one fma
+// per exp2 argument; only the last key group is bounds-checked.
+// kGroups = ceil(k_seq / 32). Visibility per key: key < k_seq, key mask,
+// causal (key <= query); a row with no visible key is 0 (reference
+// src/cuda/flash_attention_sm80.cu:214-219).
+template <bool IsBf16, int kGroups, bool kMasked, int kWaves>
+__global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kernel(FusedAttentionParams p) {
+    constexpr int kRows = 32 * kGroups;
+    constexpr int kPerWave = 8 * kGroups / kWaves;  // 1-KiB transfers per wave (4 kGroups for K, 4 kGroups for V)
+    __shared__ __attribute__((aligned(16))) char kbuf[kRows * kRowBytes];
+    __shared__ __attribute__((aligned(16))) char vbuf[kRows * kRowBytes];
+    __shared__ __attribute__((aligned(16))) char qobuf[kWaves * 32 * kRowBytes];  // per-wave Q / O staging
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hf = lane >> 5;
+    const int col = lane & 31;
+    // XCD-aware order: workgroup ids are dealt round robin over the 8 XCDs;
+    // each XCD takes a contiguous range of chunks, so the chunks of one head
+    // read its K/V through one L2.
+    int task;
+    {
+        const int n = p.total_blocks, id = (int)blockIdx.x;
+        const int xcd = id & 7, slot = id >> 3, per = n >> 3, extra = n & 7;
+        task = xcd * per + (xcd < extra ? xcd : extra) + slot;
+    }
+    const int bh = task / p.short_chunks;
+    const int blk_begin = (task % p.short_chunks) * p.short_chunk_blocks;
+    const int blk_end = min(blk_begin + p.short_chunk_blocks, p.q_blocks);
+    const int h = bh % p.heads;
+    const int b = bh / p.heads;
+    const int64_t elem = 2;
+    const char* qbase = (const char*)p.q + ((int64_t)b * p.q_seq * p.q_row_stride + (int64_t)h * kHeadDim) * elem;
+    const char* kbase = (const char*)p.k + ((int64_t)b * p.k_seq * p.k_row_stride + (int64_t)h * kHeadDim) * elem;
+    const char* vbase = (const char*)p.v + ((int64_t)b * p.k_seq * p.v_row_stride + (int64_t)h * kHeadDim) * elem;
+    char* obase = (char*)p.o + ((int64_t)b * p.q_seq * p.o_row_stride + (int64_t)h * kHeadDim) * elem;
+
+    // K/V rows into LDS (swizzled 128-byte rows as in the tiled kernel); rows
+    // past k_seq re-read the last key and are never visible.
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {
+        const int n = wave * kPerWave + j;
+        const bool is_v = n >= 4 * kGroups;
+        const int r8 = is_v ? n - 4 * kGroups : n;
+        const int row = 8 * r8 + (lane >> 3);
+        const int key = min(row, p.k_seq - 1);
+        const uint32_t stride = (uint32_t)((is_v ? p.v_row_stride : p.k_row_stride) * elem);
+        const uint32_t off = __umul24((uint32_t)key, stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+        lds_dma16(is_v ? vbase : kbase, off, lds_addr((is_v ? vbuf : kbuf) + 8 * r8 * kRowBytes));
+    }
+
+    // Q rows move HBM -> registers -> a wave-private LDS buffer in whole
+    // 128-byte row segments (8 lanes per row, 16 B each: coalesced), and the
+    // output leaves the same way; rows are stored swizzled as the K tiles.
+    // qraw[j]: row 8j + lane / 8 of the block, 16-byte chunk lane % 8.
+    auto load_q_rows = [&](int first_row, u32x4 (&qraw)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = first_row + 8 * j + (lane >> 3);
+            qraw[j] = row < p.q_seq ? *(const u32x4*)(qbase + (int64_t)row * p.q_row_stride * elem + 16 * (lane & 7))
+                                    : u32x4{0, 0, 0, 0};
+        }
+    };
+    char* wbuf = qobuf + wave * (32 * kRowBytes);
+    int blk = blk_begin + wave;
+    u32x4 qnext[4];
+    load_q_rows(32 * blk, qnext);
+    // Visibility words of keys lane and lane + 64 (wave-uniform ballots):
+    // key < k_seq and, with a key mask, mask != 0.
+    uint64_t vis_word[2] = {~0ull, ~0ull};
+    if constexpr (kMasked) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const int key = 64 * w + lane;
+            const bool ok = key < p.k_seq && (p.key_mask == nullptr || p.key_mask[(int64_t)b * p.k_seq + key] != 0);
+            vis_word[w] = __builtin_amdgcn_ballot_w64(ok);
+        }
+    }
+    wait_vmem_all();
+    __syncthreads();
+
+    const int k_swz = swz(col);
+    const int g16 = lane & 15;
+    const int tr_key = 4 * hf + (g16 >> 2), tr_qd = g16 & 3;
+    int v_off[2][2];  // [dt][second read]
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+        const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + (tr_qd >> 1);
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi)
+            v_off[dt][hi] = (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) + ((tr_qd & 1) << 3);
+    }
+    const float c = p.scale_log2;
+
+    for (; blk < blk_end; blk += kWaves) {
+        const int my_query = 32 * blk + col;
+        // park this block's Q rows, start the next block's loads (in flight
+        // during this block), read the Q^T operand: lane holds dims
+        // 16ks + 8hf .. +7 of query row col (used as stored: the softmax scale
+        // is applied in fp32 to the scores, folded into the exp2 argument).
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            *(lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4)) = qnext[j];
+        }
+        if (blk + kWaves < blk_end) load_q_rows(32 * (blk + kWaves), qnext);
+        i16x8 qop[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qop[ks] = *(const lds_i16x8*)(wbuf + col * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
+
+        // S^T[key][q] = K Q^T (unscaled), key group g: lane holds keys
+        // 32g + 8(i >> 2) + 4hf + (i & 3) of its query in s[g][i]. The groups'
+        // chains are interleaved so the matrix pipe always has independent work.
+        auto k_operand = [&](int g, int ks) __attribute__((always_inline)) {
+            return *(const lds_i16x8*)(kbuf + (32 * g + col) * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
+        };
+        f32x16 s[kGroups];
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            f32x16 z;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+            s[g] = mfma32<IsBf16>(k_operand(g, 0), qop[0], z);
+        }
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks)
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) s[g] = mfma32<IsBf16>(k_operand(g, ks), qop[ks], s[g]);
+        if constexpr (kMasked) {
+            // element i of group g is key 32g + 4hf + kk, kk = 8(i >> 2) + (i & 3)
+            const int causal_lim = p.causal ? my_query - 4 * hf : 0x7FFFFFFF;
+#pragma unroll
+            for (int g = 0; g < kGroups; ++g) {
+                const uint32_t lane_vis = (uint32_t)(vis_word[g >> 1] >> (32 * (g & 1) + 4 * hf));
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kk = 8 * (i >> 2) + (i & 3);
+                    const bool ok = ((lane_vis >> kk) & 1u) && 32 * g + kk <= causal_lim;
+                    s[g][i] = ok ? s[g][i] : -__builtin_inff();
+                }
+            }
+        } else if (p.k_seq % 32 != 0) {
+            // only the last group can hold keys past k_seq
+            const int lim = p.k_seq - 32 * (kGroups - 1) - 4 * hf;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                s[kGroups - 1][i] = 8 * (i >> 2) + (i & 3) < lim ? s[kGroups - 1][i] : -__builtin_inff();
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[g][i]);
+        mx = xhalf_max(mx);
+        // p = 2^(c s - c max), c = scale log2(e); no visible key: every p is 0
+        const float neg_cm = mx == -__builtin_inff() ? 0.0f : -c * mx;
+
+        // O^T = V^T P^T, one accumulator per d tile; V^T operands by
+        // transposing LDS reads (addresses as in the tiled kernel).
+        f32x16 out[2];
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) out[dt][i] = 0.0f;
+        float l = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g) {
+            float e[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c, neg_cm));
+            l += sum8(e) + sum8(e + 8);
+#pragma unroll
+            for (int ss = 0; ss < 2; ++ss) {
+                const i16x8 pop = __builtin_bit_cast(
+                    i16x8, u32x4{pack2<IsBf16>(e[8 * ss], e[8 * ss + 1]), pack2<IsBf16>(e[8 * ss + 2], e[8 * ss + 3]),
+                                 pack2<IsBf16>(e[8 * ss + 4], e[8 * ss + 5]), pack2<IsBf16>(e[8 * ss + 6], e[8 * ss + 7])});
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const char* base = vbuf + (32 * g + 16 * ss) * kRowBytes;
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+                    out[dt] = mfma32<IsBf16>(i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pop, out[dt]);
+                }
+            }
+        }
+        const float l_tot = xhalf_sum(l);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        // O rows through the staging buffer (its Q rows are consumed): lane
+        // holds dims 32dt + 8u + 4hf .. +3 of row col, i.e. half hf of chunk
+        // 4dt + u; then whole row segments to HBM.
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t w0 = pack2<IsBf16>(out[dt][4 * u] * inv, out[dt][4 * u + 1] * inv);
+                const uint32_t w1 = pack2<IsBf16>(out[dt][4 * u + 2] * inv, out[dt][4 * u + 3] * inv);
+                *(lds_u32x2*)(wbuf + col * kRowBytes + (((4 * dt + u) ^ k_swz) << 4) + 8 * hf) = u32x2{w0, w1};
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            const u32x4 w = *(const lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+            if (32 * blk + row < p.q_seq)
+                *(u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)) = w;
+        }
+    }
+}
+
+template <bool IsBf16, bool kMasked, int kWaves>
+hipError_t launch_short_keys_w(FusedAttentionParams p, int compute_units, hipStream_t stream) {
+    // Chunks: about two workgroups per CU in total (measured best of 1-8 on
+    // the 77-token shapes), each a run of consecutive 32-row blocks of one
+    // head, a whole number of blocks per wave (longer chunks amortise the K/V
+    // staging and let each wave prefetch its next block).
+    p.q_blocks = (p.q_seq + 31) / 32;
+    const int64_t heads_total = (int64_t)p.heads * p.batch;
+    const int64_t all_blocks = (int64_t)p.q_blocks * heads_total;
+    const int64_t target_wgs = (int64_t)(compute_units > 0 ? compute_units : 256) * 2;
+    int64_t chunk = (all_blocks + target_wgs - 1) / target_wgs;
+    chunk = (chunk + kWaves - 1) / kWaves * kWaves;  // whole rounds of the workgroup's waves
+    chunk = chunk > p.q_blocks ? p.q_blocks : chunk;
+    p.short_chunk_blocks = (int32_t)chunk;
+    p.short_chunks = (int32_t)((p.q_blocks + chunk - 1) / chunk);
+    const int64_t grid_size = heads_total * p.short_chunks;
+    if (grid_size > INT32_MAX) return hipErrorInvalidValue;
+    p.total_blocks = (int32_t)grid_size;
+    const dim3 grid(p.total_blocks), block(64 * kWaves);
+    switch ((p.k_seq + 31) / 32) {
+    case 1: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 1, kMasked, kWaves>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 2, kMasked, kWaves>), grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 3, kMasked, kWaves>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 4, kMasked, kWaves>), grid, block, 0, stream, p); break;
+    }
+    return hipGetLastError();
+}
+
+template <bool IsBf16, bool kMasked>
+hipError_t launch_short_keys(const FusedAttentionParams& p, int compute_units, hipStream_t stream) {
+    return launch_short_keys_w<IsBf16, kMasked, 4>(p, compute_units, stream);
+}
+
 }  // namespace
 
 int fused_attention_block_queries() { return 32 * kFusedWaves; }
@@ -657,6 +910,11 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     p.q_blocks = (p.q_seq + kBlockQueries - 1) / kBlockQueries;
     p.total_blocks = p.q_blocks * p.heads * p.batch;
     if (p.total_blocks == 0) return hipSuccess;
+    if (p.k_seq > 0 && p.k_seq <= kShortKeysMax) {
+        const bool masked = p.causal || p.key_mask != nullptr;
+        if (is_bf16) return masked ? launch_short_keys<true, true>(p, compute_units, stream) : launch_short_keys<true, false>(p, compute_units, stream);
+        return masked ? launch_short_keys<false, true>(p, compute_units, stream) : launch_short_keys<false, false>(p, compute_units, stream);
+    }
     // Work split. Three workgroups are resident per CU (occupancy 3, one wave
     // per SIMD each), S = 3 CUs slots. With U 128-row units, the rounds that
     // fill every slot run whole workgroups; the remaining R = U mod S units are

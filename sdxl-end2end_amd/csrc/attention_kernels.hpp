@@ -8,6 +8,8 @@ namespace sdxl_hip {
 
 // Waves per workgroup of the fused kernel (32 query rows per wave).
 constexpr int kFusedWaves = 4;
+// Key sequences up to this length run the one-pass short-key kernel (K/V wholly in LDS).
+constexpr int kShortKeysMax = 128;
 
 struct FusedAttentionParams {
     const void* q;
@@ -29,6 +31,8 @@ struct FusedAttentionParams {
     float scale_log2;      // softmax scale * log2(e)
     int32_t whole_units;   // filled by the launcher: 128-row workgroups (ids first)
     int32_t split_units;   // filled by the launcher: 64-row key-split workgroups
+    int32_t short_chunk_blocks;  // filled by the short-key launcher: 32-row blocks per workgroup
+    int32_t short_chunks;        // filled by the short-key launcher: workgroups per (batch, head)
 };
 
 // head_dim 64, fp16 or bf16 storage, 16-byte aligned rows.

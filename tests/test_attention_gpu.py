@@ -318,3 +318,56 @@ def test_key_split_workgroups(B, Sq, Sk, H):
         tref = torch_reference(qb, kb, vb, H)
         assert_parity(got, tref, label="split torch")
     assert (run(qb, kb, vb, H) == got).all()
+
+
+# ---------------------------------------------------------------- short key sequences (k_seq <= 128)
+# One-pass kernel with K/V wholly in LDS: the 77-token cross-attention and CLIP's causal
+# self-attention (src/cuda/text_encoder.cpp:83, 77 tokens).
+
+@pytest.mark.parametrize("sk", [1, 2, 31, 32, 33, 64, 77, 96, 127, 128])
+def test_short_keys_lengths(sk):
+    _check_config(2, 200, sk, 3, seed=900 + sk)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sk", [77, 128])
+def test_short_keys_mask_and_causal(causal, sk):
+    B, H = 2, 2
+    sq = sk  # causal self-attention over the token sequence, as in the text encoder
+    qb, kb, vb = seeded(910, B, sq, 128), seeded(911, B, sk, 128), seeded(912, B, sk, 128)
+    mask = (np.random.default_rng(5).random((B, sk)) > 0.3).astype(np.int32)
+    mask[1, :] = 0
+    got = run(qb, kb, vb, H, causal=causal, key_mask=torch.from_numpy(mask).to(DEV))
+    ref = oracle.attention_f16(qb, kb, vb, H, key_mask=mask, causal=causal)
+    assert_parity(got, ref, label=f"short mask causal={causal} sk={sk}")
+    assert (got[1] == 0).all()
+
+
+def test_short_keys_clip_causal():
+    """CLIP-L text encoder self-attention: 77 tokens, 12 heads, causal, no key mask."""
+    qb, kb, vb = seeded(920, 2, 77, 768), seeded(921, 2, 77, 768), seeded(922, 2, 77, 768)
+    got = run(qb, kb, vb, 12, causal=True)
+    assert_parity(got, oracle.attention_f16(qb, kb, vb, 12, causal=True), label="clip causal")
+
+
+def test_short_keys_bf16_and_strides():
+    B, S, Sk, H = 2, 300, 77, 2
+    W = H * 64
+    qb = oracle.normal_f16(930, (B, S, W))
+    kvb = oracle.normal_f16(931, (B, Sk, 2 * W))
+    kv = to_dev(kvb)
+    out = sh.attention(to_dev(qb), kv[:, :, :W], kv[:, :, W:], H)
+    torch.cuda.synchronize()
+    ref = oracle.attention_f16(qb, np.ascontiguousarray(kvb[:, :, :W]), np.ascontiguousarray(kvb[:, :, W:]), H)
+    assert_parity(from_dev(out), ref, label="short strided")
+
+
+def test_short_keys_bf16():
+    B, S, Sk, H = 2, 256, 77, 2
+    qf = oracle.normal_f32(940, (B, S, 128))
+    kf, vf = (oracle.normal_f32(941 + i, (B, Sk, 128)) for i in range(2))
+    to_bf = lambda x: torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    qd, kd, vd = to_bf(qf), to_bf(kf), to_bf(vf)
+    got = from_dev(sh.attention(qd, kd, vd, H))
+    ref = oracle.attention_f32(qd.float().cpu().numpy(), kd.float().cpu().numpy(), vd.float().cpu().numpy(), H)
+    assert_parity(got, ref, max_abs=1e-2, mean_abs=1e-3, label="short bf16")
