@@ -33,6 +33,8 @@ struct FusedAttentionParams {
     int32_t split_units;   // filled by the launcher: 64-row key-split workgroups
     int32_t short_chunk_blocks;  // filled by the short-key launcher: 32-row blocks per workgroup
     int32_t short_chunks;        // filled by the short-key launcher: workgroups per (batch, head)
+    int32_t mixed_total;         // filled by the launcher: 32-row blocks of the call (mixed kind)
+    int32_t mixed_wgs;           // filled by the launcher: mixed workgroups
 };
 
 // head_dim 64, fp16 or bf16 storage, 16-byte aligned rows.

@@ -371,3 +371,54 @@ def test_short_keys_bf16():
     got = from_dev(sh.attention(qd, kd, vd, H))
     ref = oracle.attention_f32(qd.float().cpu().numpy(), kd.float().cpu().numpy(), vd.float().cpu().numpy(), H)
     assert_parity(got, ref, max_abs=1e-2, mean_abs=1e-3, label="short bf16")
+
+
+# ---------------------------------------------------------------- mixed 12-wave workgroups
+# Unmasked, non-causal calls with Sk % 64 == 0 whose 32-row blocks fill one round of 10-block
+# workgroups on the device (T blocks with 2467 < T <= 2560 on the MI355X's 256 CUs, e.g. the
+# north-star configs[2]) run one 12-wave workgroup per CU: 8 waves with one row block each over
+# all keys and 2 row blocks split by 32-key group, merged through LDS. Workgroups may straddle
+# two heads and the last one may be short.
+
+@pytest.mark.parametrize("B,Sq,Sk,H", [
+    (1, 3488, 64, 23),    # T = 2507: short last workgroup, heads of 109 blocks straddle often
+    (1, 3200, 640, 25),   # T = 2500: 10 blocks per workgroup, no straddle
+])
+def test_mixed_workgroups(B, Sq, Sk, H):
+    _check_config(B, Sq, Sk, H, seed=960 + H)
+
+
+def test_mixed_workgroups_ragged_rows():
+    """T = 2560 with 4090 query rows: rows past Sq in the last block of every head are not stored."""
+    B, Sq, Sk, H = 2, 4090, 4096, 10
+    qb, kb, vb = seeded(970, B, Sq, H * 64), seeded(971, B, Sk, H * 64), seeded(972, B, Sk, H * 64)
+    got = run(qb, kb, vb, H)
+    for r0, r1 in [(0, 32), (2016, 2080), (4060, 4090)]:
+        ref = oracle.attention_f16_rows(qb, kb, vb, H, r0, r1)
+        assert_parity(got[:, r0:r1], ref[:, r0:r1], label=f"mixed ragged rows {r0}:{r1}")
+    assert_parity(got, torch_reference(qb, kb, vb, H), label="mixed ragged torch")
+
+
+def test_mixed_workgroups_bf16():
+    B, Sq, Sk, H = 2, 4096, 1024, 10
+    qf, kf, vf = (oracle.normal_f32(980 + i, (B, s, H * 64)) for i, s in enumerate((Sq, Sk, Sk)))
+    to_bf = lambda x: torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    qd, kd, vd = to_bf(qf), to_bf(kf), to_bf(vf)
+    got = sh.attention(qd, kd, vd, H).float()
+    torch.cuda.synchronize()
+    ref = torch_reference_bf16(qd, kd, vd, H)
+    mx = (got - ref).abs().max().item()
+    mean = (got - ref).abs().mean().item()
+    print(f"mixed bf16: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
+    assert mx <= 1e-2 and mean <= 1e-3
+
+
+def torch_reference_bf16(q, k, v, heads):
+    """FP32 attention of bf16 device tensors [B, S, H*64] with torch (scale 1/8)."""
+    B, Sq, W = q.shape
+    D = W // heads
+    qf = q.float().view(B, Sq, heads, D).transpose(1, 2)
+    kf = k.float().view(B, -1, heads, D).transpose(1, 2)
+    vf = v.float().view(B, -1, heads, D).transpose(1, 2)
+    p = torch.softmax(qf @ kf.transpose(-1, -2) / 8.0, dim=-1)
+    return (p @ vf).transpose(1, 2).reshape(B, Sq, W)
