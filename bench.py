@@ -28,6 +28,7 @@ sys.path.insert(0, os.path.join(ROOT, "sdxl-end2end_amd"))
 
 METRIC = "attention TFLOP/s + µs/call, SDXL 4096-tok self-attn b2 h10 d64 fp16"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_attention_c3_traffic.txt")
 
@@ -143,6 +144,13 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
                                                      out=y.view(M, W)),
                                    sh.linear_flops(M, W, W), 2.0 * M * W * 3 + 2.0 * W * W),
     }
+    # optional fp8-activation QKV: E4M3 LayerNorm output, E4M3 x E4M3 projection on fp8 MFMA
+    codes, cscale = sh.layer_norm_e4m3(x, gamma, beta)
+    fp8_stages = {
+        "layer_norm_e4m3": (lambda: sh.layer_norm_e4m3(x, gamma, beta), 0.0, 3.0 * M * W + 4.0 * M),
+        "qkv_e4m3_fp8_mfma": (lambda: sh.linear_e4m3(codes.view(M, W), cscale, q8, s8, out=qkv),
+                              sh.linear_flops(M, 3 * W, W), 1.0 * M * W + 3 * W * W + 2.0 * M * 3 * W),
+    }
     out = {"shape": [B, S, W], "heads": H, "w_qkv": "E4M3 [1920, 640] per-channel scales",
            "timing": "device us per call, HIP graph replay", "stages": {}}
     total = 0.0
@@ -159,6 +167,17 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
                  steps, warmup)
     out["sum_of_stages_us"] = round(total * 1e3, 2)
     out["fused_call_us"] = round(ms * 1e3, 2)
+    out["fp8_activations"] = {}
+    for name, (fn, fl, by) in fp8_stages.items():
+        t = time_fn(torch, fn, steps, warmup)
+        e = {"us": round(t * 1e3, 2), "hbm_gbs": round(by / (t * 1e-3) / 1e9, 1)}
+        if fl:
+            e["tflops"] = round(fl / (t * 1e-3) / 1e12, 1)
+            e["fp8_mfma_frac"] = round(fl / (t * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)
+        out["fp8_activations"][name] = e
+    t = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws,
+                                                fp8_activations=True), steps, warmup)
+    out["fp8_activations"]["fused_call_us"] = round(t * 1e3, 2)
     return out
 
 

@@ -36,6 +36,15 @@ sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t 
                             const void* gamma, const void* beta, float eps, void* y,
                             int64_t y_row_stride, void* stream);
 
+/* LayerNorm as sdxl_layer_norm, output quantised for the fp8 projection: the
+ * normalised row (fp32) becomes E4M3 codes q [rows, width] (row stride in bytes,
+ * 0 = width) with a per-row fp32 scale q_scale [rows] = amax > 0 ?
+ * max(amax / 448, 1e-12) : 1, code = E4M3(y / scale) rounded to nearest even and
+ * saturated to +-448 (the rule of sdxl_quantize_e4m3_rows). No counterpart in the
+ * reference (its FP8 path quantises weights only); feeds sdxl_linear_e4m3. */
+sdxl_status sdxl_layer_norm_e4m3(int64_t rows, int64_t width, const void* x, int64_t x_row_stride,
+                                 const void* gamma, const void* beta, float eps, uint8_t* q,
+                                 int64_t q_row_stride, float* q_scale, void* stream);
 typedef struct sdxl_linear_desc {
     int64_t m; /* rows of a and c */
     int64_t n; /* output features (rows of w) */
@@ -58,6 +67,16 @@ typedef struct sdxl_linear_desc {
  * aligned c/bias/residual rows (SDXL widths all qualify). */
 sdxl_status sdxl_linear(const sdxl_linear_desc* desc, const void* a, const void* w, const float* w_scale,
                         const void* bias, const void* residual, void* c, void* stream);
+/* sdxl_linear with FP8 activations on the fp8 matrix cores:
+ * c = (a . w^T) * a_scale[m] * w_scale[n] + bias + residual, a E4M3 codes [m, k]
+ * (desc->a_row_stride in bytes) with per-row fp32 scales a_scale [m] (as written by
+ * sdxl_layer_norm_e4m3), w E4M3 [n, k] with w_scale [n] (desc->w_dtype must be
+ * SDXL_DTYPE_E4M3). fp32 accumulation of exact fp8 products. Same shape and
+ * alignment rules as sdxl_linear. No counterpart in the reference (weight-only FP8
+ * there, src/cuda/fp8_kernels.cu:52-245); the optional fp8 QKV projection. */
+sdxl_status sdxl_linear_e4m3(const sdxl_linear_desc* desc, const uint8_t* a, const float* a_scale, const void* w,
+                             const float* w_scale, const void* bias, const void* residual, void* c,
+                             void* stream);
 
 /* Per-output-channel E4M3 quantisation of an fp16 weight [rows, cols] (the
  * reference's FP8 weight packing, src/cuda/weights.cu:119-170): scale[r] =
@@ -73,7 +92,11 @@ typedef struct sdxl_sublayer_desc {
     int32_t w_qkv_dtype; /* SDXL_DTYPE_F16 or SDXL_DTYPE_E4M3 */
     int32_t attn_backend; /* sdxl_attn_backend for the attention step */
     float ln_eps;      /* 0 means 1e-5 */
-    int32_t reserved;  /* must be 0 */
+    /* Activations of the QKV projection: SDXL_DTYPE_F16 (0: the reference's
+     * weight-only FP8, fp16 MFMA) or SDXL_DTYPE_E4M3 (LayerNorm quantises its
+     * output per row and the projection runs on the fp8 matrix cores; needs E4M3
+     * w_qkv). */
+    int32_t qkv_activations;
 } sdxl_sublayer_desc;
 
 /* Workspace the sublayer needs: batch * seq * width * 8 bytes (normalised

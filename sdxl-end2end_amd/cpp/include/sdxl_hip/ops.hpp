@@ -53,10 +53,12 @@ public:
     // hidden += to_out(attention(LN(hidden) . qkv_weight^T)) in place: the self-attention
     // half of the reference's UNet::transformer_block (src/cuda/unet.cpp:106-118) with q/k/v
     // as one projection. hidden fp16 [B, S, 64 heads]; qkv_weight [3W, W] fp16 or packed
-    // E4M3; out_weight [W, W] fp16; out_bias [W].
+    // E4M3; out_weight [W, W] fp16; out_bias [W]. fp8_activations (packed E4M3 qkv_weight
+    // only): LayerNorm quantises its output per row to E4M3 and the projection runs on the
+    // fp8 matrix cores (no counterpart in the reference, whose FP8 path is weight-only).
     void attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
                             const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
-                            std::size_t heads) const;
+                            std::size_t heads, bool fp8_activations = false) const;
 
 private:
     const Runtime* runtime_ = nullptr;

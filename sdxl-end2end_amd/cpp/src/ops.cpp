@@ -192,7 +192,7 @@ Tensor Ops::concat_rows(const Tensor& a, const Tensor& b, const Tensor& c) const
 
 void Ops::attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
                              const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
-                             std::size_t heads) const {
+                             std::size_t heads, bool fp8_activations) const {
     if (hidden.type() != ScalarType::Float16 || hidden.rank() != 3 || heads == 0 || hidden.size(2) != heads * 64)
         throw HipError("attention sublayer requires fp16 hidden [B, S, 64 * heads]");
     const std::size_t W = hidden.size(2);
@@ -204,16 +204,18 @@ void Ops::attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Te
     const bool fp8 = qkv_weight.type() == ScalarType::Float8E4M3;
     if (fp8 && (!qkv_weight.has_dequant_scale() || qkv_weight.dequant_scale_count() != 3 * W))
         throw HipError("FP8 weight has invalid scaling metadata");
+    if (fp8_activations && !fp8) throw HipError("FP8 activations require a packed E4M3 qkv weight");
     sdxl_sublayer_desc d{};
     d.batch = static_cast<std::int64_t>(hidden.size(0));
     d.seq = static_cast<std::int64_t>(hidden.size(1));
     d.heads = static_cast<std::int64_t>(heads);
     d.w_qkv_dtype = fp8 ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
     d.attn_backend = static_cast<std::int32_t>(runtime_->options().attention_backend);
+    d.qkv_activations = fp8_activations ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
     const std::size_t ws_bytes = sdxl_attn_sublayer_workspace_bytes(&d);
     Tensor workspace = Tensor::allocate(*runtime_, {ws_bytes}, ScalarType::Float8E4M3);  // raw bytes
     std::ostringstream label;
-    label << "unet/attention_sublayer/s" << hidden.size(1) << "_h" << heads << (fp8 ? "_e4m3" : "_f16");
+    label << "unet/attention_sublayer/s" << hidden.size(1) << "_h" << heads << (fp8_activations ? "_e4m3a" : fp8 ? "_e4m3" : "_f16");
     const int scope = runtime_->begin_profile(label.str());
     const sdxl_status st = sdxl_attn_sublayer(
         &d, hidden.data(), norm_weight.data(), norm_bias.data(), qkv_weight.data(),

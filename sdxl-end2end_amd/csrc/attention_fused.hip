@@ -258,15 +258,21 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     const float c = p.scale_log2;
     // Q^T operand, pre-scaled by scale*log2(e) so that the MFMA yields scores
     // directly in log2 units: lane holds dims 16*ks + 8*hf .. +7 of its query.
+    // The loads are issued here; the scaling (which waits for them) runs after
+    // the first K/V transfers are issued, so the two latencies overlap.
     i16x8 qop[4];
     if (my_query < p.q_seq) {
         const i16x8* qrow = (const i16x8*)(qbase + (int64_t)my_query * p.q_row_stride * elem);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qop[ks] = scale_operand<IsBf16>(qrow[2 * ks + hf], c);
+        for (int ks = 0; ks < 4; ++ks) qop[ks] = qrow[2 * ks + hf];
     } else {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qop[ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
+    auto scale_q = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qop[ks] = scale_operand<IsBf16>(qop[ks], c);
+    };
 
     // Key range. Causal: keys beyond the block's last query are never visible.
     int n_keys = p.k_seq;
@@ -581,6 +587,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // start instead of prefetching them a step earlier.
         issue_split(0, 0);
         issue_split(1, -1);
+        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], khalf, kop);
@@ -611,6 +618,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // tile (as the key-split kind); one barrier per tile step for all.
         issue_mixed(0, 0);
         issue_mixed(1, -1);
+        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], khalf, kop);
@@ -660,6 +668,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     if (n_tiles > 0) {
         issue(0, 0);
         issue(1, -1);
+        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], 0, kop);

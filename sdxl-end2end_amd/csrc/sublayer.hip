@@ -22,6 +22,13 @@
 //   and writes y with 8-byte accesses. fp32 accumulation, one rounding to fp16.
 //   LDS rows are 128 B with the chunk swizzle of the attention kernel
 //   (conflict-free 16-byte operand reads).
+//
+// FP8 activations (E4M3 codes with per-row scales, from the E4M3 LayerNorm)
+// times E4M3 weights run on the gfx950 fp8 matrix cores
+// (v_mfma_f32_32x32x64_f8f6f4, twice the fp16 rate): both operands stay as
+// codes in 64-byte LDS rows and one MFMA covers a whole 64-deep K stage; the
+// epilogue applies a_scale[m] * w_scale[n] in fp32. No reference counterpart
+// (its FP8 path is weight-only); an optional mode of the QKV projection.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -38,6 +45,11 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+struct u32x4x2 {
+    u32x4 lo, hi;
+};
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
 typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 typedef __attribute__((address_space(3))) char lds_char;
@@ -86,20 +98,31 @@ __device__ __forceinline__ void wait_vmem() {
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
 }
 
+// E4M3 x E4M3 MFMA, 32 x 32 x 64: each lane supplies 32 consecutive K bytes of
+// its row of A and of B. The hardware's K order inside an operand is the same
+// for A and B, so any fixed byte order that both operands share gives the
+// same sum.
+__device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // One workgroup = 4 waves in a 2 x 2 arrangement = a (64 kTM) x 128 output
 // tile; each wave computes (32 kTM) x 64 as kTM x 2 MFMA tiles. kRing LDS
 // stages of kBK = 64 columns of K: stage s + kRing - 1 is requested while
 // stage s is consumed (prefetch distance kRing - 1 stages), so that a stage's
 // transfers have MFMA work to land behind. E4M3 weights stay as codes in LDS
 // (64-byte rows, chunk swizzle (row >> 2) & 3) and are decoded when the
-// operand is read; fp16 weights use the A-operand layout.
-template <bool kWFp8, int kTM, int kRing, int kOcc>
+// operand is read; fp16 weights use the A-operand layout. kAFp8 (with kWFp8):
+// E4M3 activations in 64-byte rows, fp8 MFMA.
+template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc>
 __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
+    static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
     constexpr int kBMt = 64 * kTM;
     constexpr int kWRowBytes = kWFp8 ? 64 : kRowBytes;
-    constexpr int kATileBytes = kBMt * kRowBytes;
+    constexpr int kARowBytes = kAFp8 ? 64 : kRowBytes;
+    constexpr int kATileBytes = kBMt * kARowBytes;
     constexpr int kWTileBytes = 128 * kWRowBytes;
-    constexpr int kAXfers = kBMt / 32;               // 1-KiB A transfers per wave and stage
+    constexpr int kAXfers = kAFp8 ? kBMt / 64 : kBMt / 32;  // 1-KiB A transfers per wave and stage
     constexpr int kWXfers = kWFp8 ? 2 : 4;
     constexpr int kLoadsPerStage = kAXfers + kWXfers;
     // Stage st: A tile at smem[st], W tile right after it. The epilogue
@@ -125,8 +148,8 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     const int m0 = mb * kBMt, n0 = nb * kBN;
     const int n_stages = p.k / kBK;
 
-    const char* abase = (const char*)p.a + (int64_t)m0 * p.lda * 2;
-    const int64_t lda_b = p.lda * 2;
+    const int64_t lda_b = kAFp8 ? p.lda : p.lda * 2;
+    const char* abase = (const char*)p.a + (int64_t)m0 * lda_b;
     const int64_t ldw_b = kWFp8 ? p.ldw : p.ldw * 2;
     const char* wbase = (const char*)p.w + (int64_t)n0 * ldw_b;
     const int a_rows = p.m - 1 - m0, w_rows = p.n - 1 - n0;  // last valid tile row
@@ -155,19 +178,25 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     };
     // 64-byte rows (E4M3 W): transfer n covers rows 16n .. 16n+15; lane l takes
     // row 16n + l/4 and global chunk (l%4) ^ ((row >> 2) & 3).
-    auto dma_rows64 = [&](int kbyte, char* buf, int n) __attribute__((always_inline)) {
+    auto dma_rows64 = [&](const char* gbase, int64_t ld_b, int last, int kbyte, char* buf, int n)
+                          __attribute__((always_inline)) {
         const int row = 16 * n + (lane >> 2);
-        const uint32_t off = (uint32_t)(min(row, w_rows) * ldw_b) + (uint32_t)(((lane & 3) ^ ((row >> 2) & 3)) << 4);
-        lds_dma16(wbase + kbyte, off, lds_addr(buf + 16 * n * 64));
+        const uint32_t off = (uint32_t)(min(row, last) * ld_b) + (uint32_t)(((lane & 3) ^ ((row >> 2) & 3)) << 4);
+        lds_dma16(gbase + kbyte, off, lds_addr(buf + 16 * n * 64));
     };
     auto issue_stage = [&](int st) __attribute__((always_inline)) {
         char* ab = smem[st % kRing];
         char* wb = smem[st % kRing] + kATileBytes;
+        if constexpr (kAFp8) {
 #pragma unroll
-        for (int j = 0; j < kAXfers; ++j) dma_rows128(abase, lda_b, a_rows, st * kBK * 2, ab, wave * kAXfers + j);
+            for (int j = 0; j < kAXfers; ++j) dma_rows64(abase, lda_b, a_rows, st * kBK, ab, wave * kAXfers + j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < kAXfers; ++j) dma_rows128(abase, lda_b, a_rows, st * kBK * 2, ab, wave * kAXfers + j);
+        }
         if constexpr (kWFp8) {
 #pragma unroll
-            for (int j = 0; j < kWXfers; ++j) dma_rows64(st * kBK, wb, wave * kWXfers + j);
+            for (int j = 0; j < kWXfers; ++j) dma_rows64(wbase, ldw_b, w_rows, st * kBK, wb, wave * kWXfers + j);
         } else {
 #pragma unroll
             for (int j = 0; j < kWXfers; ++j) dma_rows128(wbase, ldw_b, w_rows, st * kBK * 2, wb, wave * kWXfers + j);
@@ -187,8 +216,8 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
 #pragma unroll
     for (int t = 0; t < kTM; ++t) {
         const int ar = wm * 32 * kTM + 32 * t + col;
-        a_off[t] = ar * kRowBytes;
-        a_swz[t] = swz(ar);
+        a_off[t] = ar * kARowBytes;
+        a_swz[t] = kAFp8 ? (ar >> 2) & 3 : swz(ar);
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -217,6 +246,25 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
         if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
         const char* ab = smem[s % kRing];
         const char* wb = smem[s % kRing] + kATileBytes;
+        if constexpr (kAFp8) {
+            // one fp8 MFMA per tile pair covers the stage: lane reads bytes
+            // 32hf .. +31 (chunks 2hf, 2hf + 1) of its W row and A row.
+            auto op32 = [&](const char* tile, int off, int sw) __attribute__((always_inline)) {
+                const u32x4 lo = *(const lds_u32x4*)(tile + off + (((2 * hf) ^ sw) << 4));
+                const u32x4 hi = *(const lds_u32x4*)(tile + off + (((2 * hf + 1) ^ sw) << 4));
+                return __builtin_bit_cast(i32x8, u32x4x2{lo, hi});
+            };
+            i32x8 wop8[2], aop8[kTM];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) wop8[t] = op32(wb, w_off[t] - hf * 8, w_swz[t]);
+#pragma unroll
+            for (int t = 0; t < kTM; ++t) aop8[t] = op32(ab, a_off[t], a_swz[t]);
+#pragma unroll
+            for (int i = 0; i < kTM; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[j][i] = mfma32_fp8(wop8[j], aop8[i], acc[j][i]);
+            continue;
+        }
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             i16x8 aop[kTM], wop[2];
@@ -257,8 +305,12 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     for (int i = 0; i < kTM; ++i) {
         const int rm0 = m0 + wm * 32 * kTM + 32 * i + (lane >> 4);  // row of iteration it: rm0 + 4 it
         f16x4 res[8];
+        float rs[8];  // activation scale of the row (1 for fp16 activations)
 #pragma unroll
-        for (int it = 0; it < 8; ++it) res[it] = f16x4{0, 0, 0, 0};
+        for (int it = 0; it < 8; ++it) {
+            res[it] = f16x4{0, 0, 0, 0};
+            rs[it] = kAFp8 ? p.a_scale[min(rm0 + 4 * it, p.m - 1)] : 1.0f;
+        }
         if (p.residual != nullptr && en_ok) {
 #pragma unroll
             for (int it = 0; it < 8; ++it) {
@@ -281,10 +333,10 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 const int m = rm0 + 4 * it;
                 if (m < p.m) {
                     const f32x4 a = *(const lds_f32x4*)(eb + r * 256 + ((ec ^ (r & 15)) << 4));
-                    const float v0 = a[0] * e_scale.x + e_bias.x + (float)res[it][0];
-                    const float v1 = a[1] * e_scale.y + e_bias.y + (float)res[it][1];
-                    const float v2 = a[2] * e_scale.z + e_bias.z + (float)res[it][2];
-                    const float v3 = a[3] * e_scale.w + e_bias.w + (float)res[it][3];
+                    const float v0 = a[0] * rs[it] * e_scale.x + e_bias.x + (float)res[it][0];
+                    const float v1 = a[1] * rs[it] * e_scale.y + e_bias.y + (float)res[it][1];
+                    const float v2 = a[2] * rs[it] * e_scale.z + e_bias.z + (float)res[it][2];
+                    const float v3 = a[3] * rs[it] * e_scale.w + e_bias.w + (float)res[it][3];
                     *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en) =
                         f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
                 }
@@ -324,7 +376,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 // kPer fp16 pairs per lane (width <= 128 kPer): straight-line code, every
 // load issued before the first use (indices clamped, values masked), so one
 // memory round trip covers the row.
-template <int kPer>
+// kE4M3: the normalised row (fp32) is quantised to E4M3 codes with a per-row
+// scale max(amax / 448, 1e-12) (1 for an all-zero row), round to nearest even,
+// saturated to +-448 (the weight quantiser's rule), for the fp8 projection.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+    return x;
+}
+
+template <int kPer, bool kE4M3>
 __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -357,6 +418,33 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     }
     const float var = fmaxf(wave_sum(sq) * inv_w, 0.0f);
     const float inv = 1.0f / sqrtf(var + p.eps);
+    if constexpr (kE4M3) {
+        float yv[2 * kPer];
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int c = lane + 64 * j;
+            const f16x2 gg = g[min(c, pairs - 1)], bb = bt[min(c, pairs - 1)];
+            yv[2 * j] = (v[2 * j] - mean) * inv * (float)gg[0] + (float)bb[0];
+            yv[2 * j + 1] = (v[2 * j + 1] - mean) * inv * (float)gg[1] + (float)bb[1];
+            if (c < pairs) amax = fmaxf(amax, fmaxf(fabsf(yv[2 * j]), fabsf(yv[2 * j + 1])));
+        }
+        amax = wave_max(amax);
+        const float scale = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
+        if (lane == 0) p.y_scale[row] = scale;
+        uint16_t* q = (uint16_t*)((uint8_t*)p.y + row * p.ldy);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int c = lane + 64 * j;
+            if (c < pairs) {
+                // y / scale correctly rounded, as the weight quantiser divides
+                const float q0 = fminf(fmaxf(yv[2 * j] / scale, -448.0f), 448.0f);
+                const float q1 = fminf(fmaxf(yv[2 * j + 1] / scale, -448.0f), 448.0f);
+                q[c] = (uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu);
+            }
+        }
+        return;
+    }
     f16x2* y = (f16x2*)((_Float16*)p.y + row * p.ldy);
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -401,6 +489,8 @@ __global__ __launch_bounds__(256) void quantize_e4m3_rows_kernel(QuantizeParams 
 
 hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_units, hipStream_t stream) {
     LinearParams p = params_in;
+    const bool a_fp8 = p.a_scale != nullptr;
+    if (a_fp8 && !w_fp8) return hipErrorInvalidValue;
     if (p.m == 0 || p.n == 0) return hipSuccess;
     if (p.k % kBK != 0 || p.n % 4 != 0) return hipErrorInvalidValue;
     p.n_blocks = (p.n + kBN - 1) / kBN;
@@ -412,11 +502,14 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
     const int64_t tasks = (int64_t)p.m_blocks * p.n_blocks;
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(256);
-    if (w_fp8) {
-        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, 4, 2, 2>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((linear_kernel<true, 2, 3, 2>), grid, block, 0, stream, p);
+    if (a_fp8) {
+        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((linear_kernel<true, true, 2, 3, 2>), grid, block, 0, stream, p);
+    } else if (w_fp8) {
+        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, false, 4, 2, 2>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((linear_kernel<true, false, 2, 3, 2>), grid, block, 0, stream, p);
     } else {
-        hipLaunchKernelGGL((linear_kernel<false, 2, 2, 2>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((linear_kernel<false, false, 2, 2, 2>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -425,9 +518,13 @@ hipError_t launch_layer_norm(const LayerNormParams& p, hipStream_t stream) {
     if (p.rows == 0) return hipSuccess;
     if (p.width % 2 != 0 || p.width <= 0 || p.width > 128 * kLnMaxPer) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
+    const bool e4m3 = p.y_scale != nullptr;
     switch ((p.width + 127) / 128) {
-#define SDXL_LN_CASE(n) \
-    case n: hipLaunchKernelGGL(layer_norm_kernel<n>, grid, block, 0, stream, p); break;
+#define SDXL_LN_CASE(n)                                                                   \
+    case n:                                                                               \
+        if (e4m3) hipLaunchKernelGGL((layer_norm_kernel<n, true>), grid, block, 0, stream, p); \
+        else hipLaunchKernelGGL((layer_norm_kernel<n, false>), grid, block, 0, stream, p);     \
+        break;
         SDXL_LN_CASE(1) SDXL_LN_CASE(2) SDXL_LN_CASE(3) SDXL_LN_CASE(4) SDXL_LN_CASE(5) SDXL_LN_CASE(6)
         SDXL_LN_CASE(7) SDXL_LN_CASE(8) SDXL_LN_CASE(9) SDXL_LN_CASE(10) SDXL_LN_CASE(11) SDXL_LN_CASE(12)
         SDXL_LN_CASE(13) SDXL_LN_CASE(14) SDXL_LN_CASE(15) SDXL_LN_CASE(16)

@@ -38,8 +38,15 @@ sdxl_status launch_status(hipError_t err, const char* what) {
 
 extern "C" {
 
-sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t x_row_stride, const void* gamma,
-                            const void* beta, float eps, void* y, int64_t y_row_stride, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared by sdxl_layer_norm and sdxl_layer_norm_e4m3 (y_scale set: E4M3 output,
+// y row stride in bytes).
+sdxl_status layer_norm_impl(const char* name, int64_t rows, int64_t width, const void* x, int64_t x_row_stride,
+                            const void* gamma, const void* beta, float eps, void* y, int64_t y_row_stride,
+                            float* y_scale, void* stream) {
     // Message of the reference's Ops::layer_norm checks (ops_kernels.cu:1431-1437).
     if (rows < 0 || width <= 0 || x_row_stride < 0 || y_row_stride < 0)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "CUDA layer norm shape/type mismatch");
@@ -48,27 +55,54 @@ sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t 
     if (ldx < width || ldy < width)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "CUDA layer norm shape/type mismatch");
     if (width % 2 != 0 || width > 2048 || ldx % 2 != 0 || ldy % 2 != 0)
-        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_layer_norm: width must be even and <= 2048");
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, std::string(name) + ": width must be even and <= 2048");
     if (rows == 0) return SDXL_STATUS_OK;
     if (x == nullptr || gamma == nullptr || beta == nullptr || y == nullptr)
-        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm: null tensor pointer");
-    if (!aligned(x, 4) || !aligned(y, 4) || !aligned(gamma, 4) || !aligned(beta, 4))
-        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_layer_norm: tensors must be 4-byte aligned");
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, std::string(name) + ": null tensor pointer");
+    if (!aligned(x, 4) || !aligned(y, 4) || !aligned(gamma, 4) || !aligned(beta, 4) ||
+        (y_scale != nullptr && !aligned(y_scale, 4)))
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, std::string(name) + ": tensors must be 4-byte aligned");
     sdxl_hip::LayerNormParams p{};
     p.x = x;
     p.gamma = gamma;
     p.beta = beta;
     p.y = y;
+    p.y_scale = y_scale;
     p.rows = rows;
     p.ldx = ldx;
     p.ldy = ldy;
     p.width = (int32_t)width;
     p.eps = eps > 0.0f ? eps : 1.0e-5f;
-    return launch_status(sdxl_hip::launch_layer_norm(p, reinterpret_cast<hipStream_t>(stream)), "sdxl_layer_norm");
+    return launch_status(sdxl_hip::launch_layer_norm(p, reinterpret_cast<hipStream_t>(stream)), name);
 }
 
-sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w, const float* w_scale,
-                        const void* bias, const void* residual, void* c, void* stream) {
+}  // namespace
+
+extern "C" {
+
+sdxl_status sdxl_layer_norm(int64_t rows, int64_t width, const void* x, int64_t x_row_stride, const void* gamma,
+                            const void* beta, float eps, void* y, int64_t y_row_stride, void* stream) {
+    return layer_norm_impl("sdxl_layer_norm", rows, width, x, x_row_stride, gamma, beta, eps, y, y_row_stride,
+                           nullptr, stream);
+}
+
+sdxl_status sdxl_layer_norm_e4m3(int64_t rows, int64_t width, const void* x, int64_t x_row_stride,
+                                 const void* gamma, const void* beta, float eps, uint8_t* q, int64_t q_row_stride,
+                                 float* q_scale, void* stream) {
+    if (rows > 0 && q_scale == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm_e4m3: null tensor pointer");
+    return layer_norm_impl("sdxl_layer_norm_e4m3", rows, width, x, x_row_stride, gamma, beta, eps, q, q_row_stride,
+                           q_scale, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared by sdxl_linear and sdxl_linear_e4m3 (a_scale set: a holds E4M3 codes,
+// a row stride in bytes).
+sdxl_status linear_impl(const sdxl_linear_desc* d, const void* a, const float* a_scale, const void* w,
+                        const float* w_scale, const void* bias, const void* residual, void* c, void* stream) {
     if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: null descriptor");
     if (d->reserved != 0) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: reserved field must be 0");
     if (d->w_dtype != SDXL_DTYPE_F16 && d->w_dtype != SDXL_DTYPE_E4M3)
@@ -82,6 +116,9 @@ sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w,
     if (lda < d->k || ldw < d->k || ldc < d->n || ldr < d->n)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_linear: row stride smaller than the row");
     const bool fp8 = d->w_dtype == SDXL_DTYPE_E4M3;
+    const bool a_fp8 = a_scale != nullptr;
+    if (a_fp8 && !fp8)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear_e4m3: weights must be E4M3");
     if (fp8 && w_scale == nullptr)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "FP8 weight has invalid scaling metadata");
     if (d->m == 0 || d->n == 0) return SDXL_STATUS_OK;
@@ -90,11 +127,13 @@ sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w,
     if (a == nullptr || w == nullptr || c == nullptr)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear: null tensor pointer");
     const int64_t w_elem = fp8 ? 1 : 2;
-    if (!aligned(a, 16) || (lda * 2) % 16 != 0 || !aligned(w, 16) || (ldw * w_elem) % 16 != 0 ||
+    const int64_t a_elem = a_fp8 ? 1 : 2;
+    if (!aligned(a, 16) || (lda * a_elem) % 16 != 0 || !aligned(w, 16) || (ldw * w_elem) % 16 != 0 ||
+        (a_fp8 && !aligned(a_scale, 4)) ||
         !aligned(c, 8) || ldc % 4 != 0 || (w_scale != nullptr && !aligned(w_scale, 16)) ||
         (bias != nullptr && !aligned(bias, 8)) || (residual != nullptr && (!aligned(residual, 8) || ldr % 4 != 0)))
         return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear: misaligned tensor or row stride");
-    if (lda * 2 * 128 > UINT32_MAX || ldw * w_elem * 128 > UINT32_MAX)
+    if (lda * a_elem * 256 > UINT32_MAX || ldw * w_elem * 128 > UINT32_MAX)
         return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_linear: row stride too large");
     sdxl_hip::LinearParams p{};
     p.a = a;
@@ -102,6 +141,7 @@ sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w,
     p.w_scale = w_scale;
     p.bias = bias;
     p.residual = residual;
+    p.a_scale = a_scale;
     p.c = c;
     p.lda = lda;
     p.ldw = ldw;
@@ -110,7 +150,25 @@ sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w,
     p.m = (int32_t)d->m;
     p.n = (int32_t)d->n;
     p.k = (int32_t)d->k;
-    return launch_status(sdxl_hip::launch_linear(p, fp8, compute_units(), reinterpret_cast<hipStream_t>(stream)), "sdxl_linear");
+    return launch_status(sdxl_hip::launch_linear(p, fp8, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                         a_fp8 ? "sdxl_linear_e4m3" : "sdxl_linear");
+}
+
+}  // namespace
+
+extern "C" {
+
+sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w, const float* w_scale,
+                        const void* bias, const void* residual, void* c, void* stream) {
+    return linear_impl(d, a, nullptr, w, w_scale, bias, residual, c, stream);
+}
+
+sdxl_status sdxl_linear_e4m3(const sdxl_linear_desc* d, const uint8_t* a, const float* a_scale, const void* w,
+                             const float* w_scale, const void* bias, const void* residual, void* c, void* stream) {
+    if (d != nullptr && d->m > 0 && a_scale == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_linear_e4m3: null activation scales");
+    if (d != nullptr && d->m == 0) return linear_impl(d, a, nullptr, w, w_scale, bias, residual, c, stream);
+    return linear_impl(d, a, a_scale, w, w_scale, bias, residual, c, stream);
 }
 
 sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, uint8_t* q, float* scales,
@@ -140,8 +198,11 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
                                const void* w_qkv, const float* w_qkv_scale, const void* w_out, const void* b_out,
                                void* y, void* workspace, size_t workspace_bytes, void* stream) {
     if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: null descriptor");
-    if (d->reserved != 0)
-        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: reserved field must be 0");
+    if (d->qkv_activations != SDXL_DTYPE_F16 && d->qkv_activations != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer: qkv_activations must be F16 or E4M3");
+    const bool act_fp8 = d->qkv_activations == SDXL_DTYPE_E4M3;
+    if (act_fp8 && d->w_qkv_dtype != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_attn_sublayer: E4M3 activations need E4M3 w_qkv");
     if (d->batch < 0 || d->seq < 0 || d->heads <= 0)
         return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_attn_sublayer: invalid shape");
     const int64_t W = d->heads * 64;
@@ -152,16 +213,26 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     char* ws = static_cast<char*>(workspace);
     void* hidden_ws = ws;                                  // [M, W]: LN output, later attention output
     void* qkv = ws + (size_t)M * (size_t)W * 2;            // [M, 3W]
-
-    sdxl_status st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
-    if (st != SDXL_STATUS_OK) return st;
+    // E4M3 activations: codes [M, W] bytes, then their row scales [M], both
+    // inside the first region (M W + 4 M <= 2 M W bytes for W >= 4).
+    uint8_t* codes = static_cast<uint8_t*>(hidden_ws);
+    float* code_scale = reinterpret_cast<float*>(ws + (size_t)M * (size_t)W);
 
     sdxl_linear_desc qd{};
     qd.m = M;
     qd.n = 3 * W;
     qd.k = W;
     qd.w_dtype = d->w_qkv_dtype;
-    st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+    sdxl_status st;
+    if (act_fp8) {
+        st = sdxl_layer_norm_e4m3(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, codes, 0, code_scale, stream);
+        if (st != SDXL_STATUS_OK) return st;
+        st = sdxl_linear_e4m3(&qd, codes, code_scale, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+    } else {
+        st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+        if (st != SDXL_STATUS_OK) return st;
+        st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+    }
     if (st != SDXL_STATUS_OK) return st;
 
     sdxl_attn_desc ad{};

@@ -16,6 +16,7 @@ struct LinearParams {
     const float* w_scale;   // nullable: 1
     const void* bias;       // nullable
     const void* residual;   // nullable
+    const float* a_scale;   // nullable; set: a holds E4M3 codes with per-row scales (w must be E4M3)
     void* c;
     int64_t lda, ldw, ldr, ldc;
     int32_t m, n, k;
@@ -29,6 +30,7 @@ struct LayerNormParams {
     const void* gamma;
     const void* beta;
     void* y;
+    float* y_scale;  // nullable; set: y receives E4M3 codes (row stride ldy bytes) and per-row scales
     int64_t rows;
     int64_t ldx, ldy;
     int32_t width;  // even, <= 2048

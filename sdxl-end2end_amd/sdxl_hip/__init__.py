@@ -30,7 +30,9 @@ EXPORTED_SYMBOLS = (
     "sdxl_last_error",
     "sdxl_abi_version",
     "sdxl_layer_norm",
+    "sdxl_layer_norm_e4m3",
     "sdxl_linear",
+    "sdxl_linear_e4m3",
     "sdxl_quantize_e4m3_rows",
     "sdxl_attn_sublayer_workspace_bytes",
     "sdxl_attn_sublayer",
@@ -71,7 +73,7 @@ class SublayerDesc(ctypes.Structure):
 
     _fields_ = [("batch", ctypes.c_int64), ("seq", ctypes.c_int64), ("heads", ctypes.c_int64),
                 ("w_qkv_dtype", ctypes.c_int32), ("attn_backend", ctypes.c_int32),
-                ("ln_eps", ctypes.c_float), ("reserved", ctypes.c_int32)]
+                ("ln_eps", ctypes.c_float), ("qkv_activations", ctypes.c_int32)]
 
 
 class SdxlError(RuntimeError):
@@ -114,8 +116,12 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     lib.sdxl_layer_norm.restype = ctypes.c_int
     lib.sdxl_layer_norm.argtypes = [i64, i64, vp, i64, vp, vp, ctypes.c_float, vp, i64, vp]
+    lib.sdxl_layer_norm_e4m3.restype = ctypes.c_int
+    lib.sdxl_layer_norm_e4m3.argtypes = [i64, i64, vp, i64, vp, vp, ctypes.c_float, vp, i64, vp, vp]
     lib.sdxl_linear.restype = ctypes.c_int
     lib.sdxl_linear.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp]
+    lib.sdxl_linear_e4m3.restype = ctypes.c_int
+    lib.sdxl_linear_e4m3.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp, vp]
     lib.sdxl_quantize_e4m3_rows.restype = ctypes.c_int
     lib.sdxl_quantize_e4m3_rows.argtypes = [i64, i64, vp, vp, vp, vp]
     lib.sdxl_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
@@ -244,6 +250,35 @@ def layer_norm(x, gamma, beta, eps: float = 1e-5, out=None):
     return out
 
 
+def layer_norm_e4m3(x, gamma, beta, eps: float = 1e-5):
+    """LayerNorm quantised for the fp8 projection: returns (codes uint8 [..., W], row scales fp32 [rows])."""
+    import torch
+    W = x.shape[-1]
+    rows = x.numel() // W if W else 0
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    s = torch.empty((rows,), dtype=torch.float32, device=x.device)
+    _check(load().sdxl_layer_norm_e4m3(rows, W, _ptr(x), x.stride(-2) if x.dim() > 1 else W, _ptr(gamma),
+                                       _ptr(beta), eps, _ptr(q), W, _ptr(s), _stream(x)))
+    return q, s
+
+
+def linear_e4m3(a, a_scale, w, w_scale, bias=None, residual=None, out=None):
+    """FP8-activation linear: a uint8 E4M3 [M, K] with row scales a_scale [M], w uint8 E4M3 [N, K]
+    with w_scale [N]; returns (a . w^T) * a_scale * w_scale + bias + residual as fp16 [M, N]."""
+    import torch
+    M, K = a.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=a.device)
+    d = LinearDesc(m=M, n=N, k=K, a_row_stride=a.stride(0), w_row_stride=w.stride(0),
+                   c_row_stride=out.stride(0),
+                   residual_row_stride=residual.stride(0) if residual is not None else 0,
+                   w_dtype=E4M3, reserved=0)
+    _check(load().sdxl_linear_e4m3(ctypes.byref(d), _ptr(a), _ptr(a_scale), _ptr(w), _ptr(w_scale), _ptr(bias),
+                                   _ptr(residual), _ptr(out), _stream(a)))
+    return out
+
+
 def linear(a, w, w_scale=None, bias=None, residual=None, out=None):
     """Ops::linear: a [M, K] fp16, w [N, K] fp16 or uint8 E4M3 codes (with w_scale [N] fp32),
     optional bias [N] and residual [M, N]; returns [M, N] fp16 (2-D views with unit column stride)."""
@@ -278,15 +313,16 @@ def sublayer_workspace_bytes(batch: int, seq: int, heads: int) -> int:
 
 
 def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads: int, out=None,
-                  workspace=None, backend: int = AUTO, eps: float = 0.0):
+                  workspace=None, backend: int = AUTO, eps: float = 0.0, fp8_activations: bool = False):
     """x + to_out(attention(LN(x) . w_qkv^T)) for hidden x [B, S, W] fp16 (reference
-    src/cuda/unet.cpp:106-118 with q/k/v fused): w_qkv [3W, W] fp16 or uint8 E4M3 + w_qkv_scale [3W]."""
+    src/cuda/unet.cpp:106-118 with q/k/v fused): w_qkv [3W, W] fp16 or uint8 E4M3 + w_qkv_scale [3W].
+    fp8_activations: LayerNorm emits E4M3 codes and the QKV projection runs on fp8 MFMA."""
     import torch
     B, S, W = x.shape
     if out is None:
         out = torch.empty_like(x)
     d = SublayerDesc(batch=B, seq=S, heads=heads, w_qkv_dtype=E4M3 if w_qkv.dtype == torch.uint8 else F16,
-                     attn_backend=backend, ln_eps=eps, reserved=0)
+                     attn_backend=backend, ln_eps=eps, qkv_activations=E4M3 if fp8_activations else F16)
     nbytes = int(load().sdxl_attn_sublayer_workspace_bytes(ctypes.byref(d)))
     if workspace is None:
         workspace = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)

@@ -190,7 +190,9 @@ def test_sublayer_workspace_and_validation():
     args = [16] * 7
     assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, None, 1 << 20, None) == sh.INVALID_ARGUMENT
     assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1024, None) == sh.INVALID_ARGUMENT  # too small
-    d.reserved = 1
+    d.qkv_activations = 7
     assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1 << 20, None) == sh.INVALID_ARGUMENT
+    d.qkv_activations = sh.E4M3  # E4M3 activations with fp16 w_qkv
+    assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1 << 20, None) == sh.UNSUPPORTED
     assert L.sdxl_quantize_e4m3_rows(-1, 4, 16, 16, 16, None) == sh.INVALID_SHAPE
     assert L.sdxl_quantize_e4m3_rows(0, 4, 0, 0, 0, None) == sh.OK
