@@ -37,7 +37,8 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # ~20 ms of untimed launches: a fresh process needs about 60 launches before the clock settles
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...) and exit")

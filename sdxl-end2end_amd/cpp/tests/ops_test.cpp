@@ -163,6 +163,14 @@ void sublayer_cases() {
     ops.linear_residual_into(attn, wod, &bod, step);
     const auto a = fused.to_host_f32(runtime).values, b = step.to_host_f32(runtime).values;
     for (std::size_t i = 0; i < a.size(); ++i) require(a[i] == b[i], "attention_sublayer == composition");
+    // fp8 activations (E4M3 LayerNorm output, fp8 MFMA projection): close to the fp16-activation result
+    auto fused8 = Tensor::from_host_f32(runtime, x);
+    ops.attention_sublayer(fused8, gd, bd, qkv8, wod, bod, heads, /*fp8_activations=*/true);
+    const auto a8 = fused8.to_host_f32(runtime).values;
+    for (std::size_t i = 0; i < a.size(); ++i) require_close(a8[i], a[i], 2e-2F, "sublayer fp8 activations");
+    const auto qkv16 = Tensor::from_host_f32(runtime, wq);
+    require_throws([&] { ops.attention_sublayer(fused8, gd, bd, qkv16, wod, bod, heads, true); },
+                   "FP8 activations require a packed E4M3 qkv weight", "fp8 activations need E4M3 weights");
     std::cout << "sublayer cases passed\n";
 }
 
