@@ -182,6 +182,51 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
     return out
 
 
+def bench_cross_sublayer(torch, sh, steps=50, warmup=5):
+    """The cross-attention half of a level-2 transformer block (32x32 latent, 20 heads): hidden
+    [2, 1024, 1280] -> LayerNorm -> to_q -> attention against the 77-token context's K|V (projected
+    once per request from [2, 77, 2048], timed separately) -> to_out + bias + residual."""
+    B, S, H, L, C = 2, 1024, 20, 77, 2048
+    W, M = H * 64, B * S
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(11)
+    x = torch.randn(B, S, W, device="cuda:0", generator=g).half()
+    gamma = torch.ones(W, dtype=torch.float16, device="cuda:0")
+    beta = torch.zeros(W, dtype=torch.float16, device="cuda:0")
+    ctx = torch.randn(B, L, C, device="cuda:0", generator=g).half()
+    w_kv = (torch.randn(2 * W, C, device="cuda:0", generator=g) * 0.02).half()
+    w_q = (torch.randn(W, W, device="cuda:0", generator=g) * 0.02).half()
+    w_out = (torch.randn(W, W, device="cuda:0", generator=g) * 0.02).half()
+    b_out = (torch.randn(W, device="cuda:0", generator=g) * 0.02).half()
+    kv = sh.project_context_kv(ctx, w_kv)
+    n = torch.empty_like(x)
+    q = torch.empty(M, W, dtype=torch.float16, device="cuda:0")
+    attn = torch.empty(B, S, W, dtype=torch.float16, device="cuda:0")
+    y = torch.empty_like(x)
+    stages = {
+        "context_kv_projection_per_request": (lambda: sh.project_context_kv(ctx, w_kv), sh.linear_flops(B * L, 2 * W, C)),
+        "layer_norm": (lambda: sh.layer_norm(x, gamma, beta, out=n), 0.0),
+        "q_projection": (lambda: sh.linear(n.view(M, W), w_q, out=q), sh.linear_flops(M, W, W)),
+        "attention_77": (lambda: sh.attention(q.view(B, S, W), kv[..., :W], kv[..., W:], H, out=attn),
+                         sh.attention_flops(B, H, S, L)),
+        "out_proj_bias_residual": (lambda: sh.linear(attn.view(M, W), w_out, bias=b_out, residual=x.view(M, W),
+                                                     out=y.view(M, W)), sh.linear_flops(M, W, W)),
+    }
+    out = {"shape": [B, S, W], "heads": H, "context": [B, L, C], "timing": "device us per call, HIP graph replay",
+           "stages": {}}
+    for name, (fn, fl) in stages.items():
+        ms = time_fn(torch, fn, steps, warmup)
+        e = {"us": round(ms * 1e3, 2)}
+        if fl:
+            e["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
+        out["stages"][name] = e
+    ws = torch.empty(2 * M * W * 2, dtype=torch.uint8, device="cuda:0")
+    ms = time_fn(torch, lambda: sh.cross_attn_sublayer(x, gamma, beta, w_q, None, kv, w_out, b_out, H, out=y,
+                                                       workspace=ws), steps, warmup)
+    out["fused_call_us"] = round(ms * 1e3, 2)
+    return out
+
+
 def ceiling(torch, sh):
     """Data-dependent throughput: the same instruction streams on N(0,1) operands and on a zero
     operand. MFMA power scales with operand toggling; on random data the device lowers its clock."""
@@ -285,6 +330,9 @@ def main():
     if args.only == "c4":
         print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
+    if args.only == "cross":
+        print(json.dumps(bench_cross_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)
@@ -344,6 +392,7 @@ def main():
                          "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
             del qq, kk, vv
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
+        sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
         result["secondary"] = sec
 
     if not args.no_cpu:

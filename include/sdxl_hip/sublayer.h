@@ -114,6 +114,36 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* desc, const void* x, co
                                const void* w_out, const void* b_out, void* y, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+typedef struct sdxl_cross_sublayer_desc {
+    int64_t batch;
+    int64_t seq;
+    int64_t heads;       /* width = heads * 64 */
+    int64_t ctx_len;     /* context tokens (77 for SDXL's CLIP context) */
+    int32_t w_q_dtype;   /* SDXL_DTYPE_F16 or SDXL_DTYPE_E4M3 */
+    int32_t attn_backend; /* sdxl_attn_backend for the attention step */
+    float ln_eps;        /* 0 means 1e-5 */
+    int32_t q_activations; /* SDXL_DTYPE_F16 or SDXL_DTYPE_E4M3 (fp8 MFMA; E4M3 w_q) */
+} sdxl_cross_sublayer_desc;
+
+/* Workspace the cross-attention sublayer needs: batch * seq * width * 4 bytes
+ * (normalised hidden / attention output, then the query projection). */
+size_t sdxl_cross_attn_sublayer_workspace_bytes(const sdxl_cross_sublayer_desc* desc);
+
+/* The cross-attention half of the reference's transformer block
+ * (src/cuda/unet.cpp:120-131): y = x + to_out(attention(LN(x) . w_q^T, K, V)) for
+ * hidden x [B, S, W] fp16. kv [B, ctx_len, 2W] fp16 holds K | V of the context,
+ * projected once per request (the context is constant over the sampler steps):
+ * sdxl_linear of encoder_hidden_states [B * ctx_len, C] against the row-concatenated
+ * [to_k; to_v] weight [2W, C]. kv_row_stride in elements (0 = 2W). w_q [W, W] fp16 or
+ * E4M3 (+ w_q_scale [W]); w_out [W, W] fp16, b_out [W]; the residual is added in
+ * the output projection's epilogue. y may equal x. workspace:
+ * sdxl_cross_attn_sublayer_workspace_bytes, 256-byte aligned. */
+sdxl_status sdxl_cross_attn_sublayer(const sdxl_cross_sublayer_desc* desc, const void* x, const void* ln_gamma,
+                                     const void* ln_beta, const void* w_q, const float* w_q_scale,
+                                     const void* kv, int64_t kv_row_stride, const void* w_out,
+                                     const void* b_out, void* y, void* workspace, size_t workspace_bytes,
+                                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,8 @@ public:
     // Rows of q, k, v projection weights [W, W] concatenated into [3W, W]
     // (fp16), the fused QKV weight attention_sublayer takes.
     [[nodiscard]] Tensor concat_rows(const Tensor& a, const Tensor& b, const Tensor& c) const;
+    // Two-weight form: [to_k; to_v] [2W, C], the context K|V projection's weight.
+    [[nodiscard]] Tensor concat_rows(const Tensor& a, const Tensor& b) const;
 
     // hidden += to_out(attention(LN(hidden) . qkv_weight^T)) in place: the self-attention
     // half of the reference's UNet::transformer_block (src/cuda/unet.cpp:106-118) with q/k/v
@@ -59,6 +61,14 @@ public:
     void attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
                             const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
                             std::size_t heads, bool fp8_activations = false) const;
+
+    // hidden += to_out(attention(LN(hidden) . q_weight^T, K, V)) in place: the cross-attention
+    // half of the reference's transformer block (src/cuda/unet.cpp:120-131). context_kv
+    // [B, L, 2W] fp16 holds K | V of encoder_hidden_states, projected once per request:
+    // linear(context, concat_rows(to_k, to_v)). q_weight [W, W] fp16 or packed E4M3.
+    void cross_attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
+                                  const Tensor& q_weight, const Tensor& context_kv, const Tensor& out_weight,
+                                  const Tensor& out_bias, std::size_t heads, bool fp8_activations = false) const;
 
 private:
     const Runtime* runtime_ = nullptr;

@@ -190,6 +190,60 @@ Tensor Ops::concat_rows(const Tensor& a, const Tensor& b, const Tensor& c) const
     return out;
 }
 
+Tensor Ops::concat_rows(const Tensor& a, const Tensor& b) const {
+    for (const Tensor* t : {&a, &b})
+        if (t->rank() != 2 || t->type() != a.type() || t->size(1) != a.size(1))
+            throw HipError("concat_rows requires rank-2 tensors of one type and width");
+    Tensor out = Tensor::allocate(*runtime_, {a.size(0) + b.size(0), a.size(1)}, a.type());
+    char* dst = static_cast<char*>(out.data());
+    for (const Tensor* t : {&a, &b}) {
+        if (t->bytes() > 0)
+            SDXL_HIP_CHECK(hipMemcpyAsync(dst, t->data(), t->bytes(), hipMemcpyDeviceToDevice, runtime_->stream()));
+        dst += t->bytes();
+    }
+    return out;
+}
+
+void Ops::cross_attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
+                                   const Tensor& q_weight, const Tensor& context_kv, const Tensor& out_weight,
+                                   const Tensor& out_bias, std::size_t heads, bool fp8_activations) const {
+    if (hidden.type() != ScalarType::Float16 || hidden.rank() != 3 || heads == 0 || hidden.size(2) != heads * 64)
+        throw HipError("attention sublayer requires fp16 hidden [B, S, 64 * heads]");
+    const std::size_t W = hidden.size(2);
+    if (q_weight.rank() != 2 || q_weight.size(0) != W || q_weight.size(1) != W ||
+        out_weight.type() != ScalarType::Float16 || out_weight.rank() != 2 || out_weight.size(0) != W ||
+        out_weight.size(1) != W || norm_weight.elements() != W || norm_bias.elements() != W ||
+        out_bias.elements() != W)
+        throw HipError("attention sublayer weight mismatch");
+    if (context_kv.type() != ScalarType::Float16 || context_kv.rank() != 3 || context_kv.size(0) != hidden.size(0) ||
+        context_kv.size(2) != 2 * W)
+        throw HipError("cross attention requires context K|V [B, L, 2W] fp16");
+    const bool fp8 = q_weight.type() == ScalarType::Float8E4M3;
+    if (fp8 && (!q_weight.has_dequant_scale() || q_weight.dequant_scale_count() != W))
+        throw HipError("FP8 weight has invalid scaling metadata");
+    if (fp8_activations && !fp8) throw HipError("FP8 activations require a packed E4M3 q weight");
+    sdxl_cross_sublayer_desc d{};
+    d.batch = static_cast<std::int64_t>(hidden.size(0));
+    d.seq = static_cast<std::int64_t>(hidden.size(1));
+    d.heads = static_cast<std::int64_t>(heads);
+    d.ctx_len = static_cast<std::int64_t>(context_kv.size(1));
+    d.w_q_dtype = fp8 ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
+    d.attn_backend = static_cast<std::int32_t>(runtime_->options().attention_backend);
+    d.q_activations = fp8_activations ? SDXL_DTYPE_E4M3 : SDXL_DTYPE_F16;
+    const std::size_t ws_bytes = sdxl_cross_attn_sublayer_workspace_bytes(&d);
+    Tensor workspace = Tensor::allocate(*runtime_, {ws_bytes}, ScalarType::Float8E4M3);  // raw bytes
+    std::ostringstream label;
+    label << "unet/cross_attention_sublayer/s" << hidden.size(1) << "_k" << context_kv.size(1) << "_h" << heads
+          << (fp8_activations ? "_e4m3a" : fp8 ? "_e4m3" : "_f16");
+    const int scope = runtime_->begin_profile(label.str());
+    const sdxl_status st = sdxl_cross_attn_sublayer(
+        &d, hidden.data(), norm_weight.data(), norm_bias.data(), q_weight.data(),
+        fp8 ? q_weight.dequant_scale_data() : nullptr, context_kv.data(), 0, out_weight.data(), out_bias.data(),
+        hidden.data(), workspace.data(), ws_bytes, runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+}
+
 void Ops::attention_sublayer(Tensor& hidden, const Tensor& norm_weight, const Tensor& norm_bias,
                              const Tensor& qkv_weight, const Tensor& out_weight, const Tensor& out_bias,
                              std::size_t heads, bool fp8_activations) const {

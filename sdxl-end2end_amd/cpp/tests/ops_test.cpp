@@ -171,6 +171,31 @@ void sublayer_cases() {
     const auto qkv16 = Tensor::from_host_f32(runtime, wq);
     require_throws([&] { ops.attention_sublayer(fused8, gd, bd, qkv16, wod, bod, heads, true); },
                    "FP8 activations require a packed E4M3 qkv weight", "fp8 activations need E4M3 weights");
+    // cross_attention_sublayer == layer_norm -> linear(q) -> attention(q, K, V of the projected
+    // context) -> linear_residual_into (the block's second half, unet.cpp:120-131)
+    const std::size_t ctx_len = 77, ctx_dim = 128;
+    const auto ctx = filled({2, ctx_len, ctx_dim}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.031F); });
+    const auto wk = filled({W, ctx_dim}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.011F) * 0.08F; });
+    const auto wv = filled({W, ctx_dim}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.019F) * 0.08F; });
+    const auto wq1 = filled({W, W}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.023F) * 0.06F; });
+    auto ctxd = Tensor::from_host_f32(runtime, ctx);
+    const auto kv = ops.linear(ctxd, ops.concat_rows(Tensor::from_host_f32(runtime, wk), Tensor::from_host_f32(runtime, wv)));
+    const auto wqd = Tensor::from_host_f32(runtime, wq1);
+    auto crossed = Tensor::from_host_f32(runtime, x);
+    ops.cross_attention_sublayer(crossed, gd, bd, wqd, kv, wod, bod, heads);
+    auto cstep = Tensor::from_host_f32(runtime, x);
+    const auto cq = ops.linear(ops.layer_norm(cstep, gd, bd), wqd);
+    const auto kvh = kv.to_host_f32(runtime);
+    FloatTensor kh2{{2, ctx_len, W}, {}}, vh2{{2, ctx_len, W}, {}};
+    for (std::size_t r = 0; r < 2 * ctx_len; ++r)
+        for (std::size_t c = 0; c < W; ++c) {
+            kh2.values.push_back(kvh.values[r * 2 * W + c]);
+            vh2.values.push_back(kvh.values[r * 2 * W + W + c]);
+        }
+    const auto cattn = ops.attention(cq, Tensor::from_host_f32(runtime, kh2), Tensor::from_host_f32(runtime, vh2), heads);
+    ops.linear_residual_into(cattn, wod, &bod, cstep);
+    const auto ca = crossed.to_host_f32(runtime).values, cb = cstep.to_host_f32(runtime).values;
+    for (std::size_t i = 0; i < ca.size(); ++i) require(ca[i] == cb[i], "cross_attention_sublayer == composition");
     std::cout << "sublayer cases passed\n";
 }
 

@@ -107,7 +107,7 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 }
 
 // One workgroup = 4 waves in a 2 x 2 arrangement = a (64 kTM) x 128 output
-// tile; each wave computes (32 kTM) x 64 as kTM x 2 MFMA tiles. kRing LDS
+// tile (kTM = 1, 2 or 4); each wave computes (32 kTM) x 64 as kTM x 2 MFMA tiles. kRing LDS
 // stages of kBK = 64 columns of K: stage s + kRing - 1 is requested while
 // stage s is consumed (prefetch distance kRing - 1 stages), so that a stage's
 // transfers have MFMA work to land behind. E4M3 weights stay as codes in LDS
@@ -127,7 +127,10 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     constexpr int kLoadsPerStage = kAXfers + kWXfers;
     // Stage st: A tile at smem[st], W tile right after it. The epilogue
     // reuses the array.
-    __shared__ __attribute__((aligned(16))) char smem[kRing][kATileBytes + kWTileBytes];
+    // (at least the epilogue's 4 x 32 x 256 bytes of staging)
+    constexpr int kStageBytes = kATileBytes + kWTileBytes;
+    constexpr int kSmemStages = kRing * kStageBytes >= 4 * 32 * 256 ? kRing : (4 * 32 * 256 + kStageBytes - 1) / kStageBytes;
+    __shared__ __attribute__((aligned(16))) char smem[kSmemStages][kStageBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -494,22 +497,31 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
     if (p.m == 0 || p.n == 0) return hipSuccess;
     if (p.k % kBK != 0 || p.n % 4 != 0) return hipErrorInvalidValue;
     p.n_blocks = (p.n + kBN - 1) / kBN;
-    // 256-row tiles (twice the MFMA work per staged byte) when they still give
-    // at least 80% of the resident workgroups (two per CU) work; else 128.
+    // Row-tile height: 256 (twice the MFMA work per staged byte, E4M3 weights)
+    // when those tiles still give at least 80% of the resident workgroups (two
+    // per CU) work; else 128, unless 128-row tiles fill less than 70% of them,
+    // then 64 (measured: 2048 x 1280 x 1280 18.3 -> 15.2 us fp16, 12.2 -> 10.0
+    // fp8; 8192 x 640 x 640 E4M3 weights 15.3 -> 13.2 us).
+    const int64_t slots = (int64_t)(compute_units > 0 ? compute_units : 256) * 2;
     const int64_t tall = (int64_t)((p.m + 255) / 256) * p.n_blocks;
-    const bool use_tall = w_fp8 && tall * 5 >= (int64_t)compute_units * 2 * 4;
-    p.m_blocks = use_tall ? (p.m + 255) / 256 : (p.m + 127) / 128;
+    const int64_t mid = (int64_t)((p.m + 127) / 128) * p.n_blocks;
+    const bool use_tall = w_fp8 && tall * 5 >= slots * 4;
+    const bool use_short = !use_tall && mid * 10 < slots * 7;
+    p.m_blocks = use_tall ? (p.m + 255) / 256 : use_short ? (p.m + 63) / 64 : (p.m + 127) / 128;
     const int64_t tasks = (int64_t)p.m_blocks * p.n_blocks;
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(256);
     if (a_fp8) {
         if (use_tall) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2>), grid, block, 0, stream, p);
+        else if (use_short) hipLaunchKernelGGL((linear_kernel<true, true, 1, 2, 2>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((linear_kernel<true, true, 2, 3, 2>), grid, block, 0, stream, p);
     } else if (w_fp8) {
         if (use_tall) hipLaunchKernelGGL((linear_kernel<true, false, 4, 2, 2>), grid, block, 0, stream, p);
+        else if (use_short) hipLaunchKernelGGL((linear_kernel<true, false, 1, 2, 2>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((linear_kernel<true, false, 2, 3, 2>), grid, block, 0, stream, p);
     } else {
-        hipLaunchKernelGGL((linear_kernel<false, false, 2, 2, 2>), grid, block, 0, stream, p);
+        if (use_short) hipLaunchKernelGGL((linear_kernel<false, false, 1, 2, 2>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((linear_kernel<false, false, 2, 2, 2>), grid, block, 0, stream, p);
     }
     return hipGetLastError();
 }

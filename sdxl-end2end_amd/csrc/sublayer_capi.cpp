@@ -1,7 +1,8 @@
-// C ABI of the attention sublayer (include/sdxl_hip/sublayer.h): validation
-// and stream-ordered launches of LayerNorm, linear, E4M3 quantisation and the
+// C ABI of the attention sublayers (include/sdxl_hip/sublayer.h): validation
+// and stream-ordered launches of LayerNorm, linear, E4M3 quantisation, the
 // whole LN -> fused QKV -> attention -> output projection + residual chain
-// (reference src/cuda/unet.cpp:106-118).
+// (reference src/cuda/unet.cpp:106-118) and its cross-attention counterpart
+// with the context K/V projected once per request (src/cuda/unet.cpp:120-131).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -247,6 +248,80 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     ad.backend = d->attn_backend;
     const char* qkv_c = static_cast<const char*>(qkv);
     st = sdxl_attn_fwd(&ad, qkv_c, qkv_c + W * 2, qkv_c + 2 * W * 2, nullptr, hidden_ws, stream);
+    if (st != SDXL_STATUS_OK) return st;
+
+    sdxl_linear_desc od{};
+    od.m = M;
+    od.n = W;
+    od.k = W;
+    od.w_dtype = SDXL_DTYPE_F16;
+    return sdxl_linear(&od, hidden_ws, w_out, nullptr, b_out, x, y, stream);
+}
+
+size_t sdxl_cross_attn_sublayer_workspace_bytes(const sdxl_cross_sublayer_desc* d) {
+    if (d == nullptr || d->batch < 0 || d->seq < 0 || d->heads < 0) return 0;
+    return (size_t)d->batch * (size_t)d->seq * (size_t)(d->heads * 64) * 4u;
+}
+
+sdxl_status sdxl_cross_attn_sublayer(const sdxl_cross_sublayer_desc* d, const void* x, const void* ln_gamma,
+                                     const void* ln_beta, const void* w_q, const float* w_q_scale, const void* kv,
+                                     int64_t kv_row_stride, const void* w_out, const void* b_out, void* y,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+    if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_cross_attn_sublayer: null descriptor");
+    if (d->q_activations != SDXL_DTYPE_F16 && d->q_activations != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT,
+                             "sdxl_cross_attn_sublayer: q_activations must be F16 or E4M3");
+    const bool act_fp8 = d->q_activations == SDXL_DTYPE_E4M3;
+    if (act_fp8 && d->w_q_dtype != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_cross_attn_sublayer: E4M3 activations need E4M3 w_q");
+    if (d->batch < 0 || d->seq < 0 || d->heads <= 0 || d->ctx_len < 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_cross_attn_sublayer: invalid shape");
+    const int64_t W = d->heads * 64;
+    const int64_t M = d->batch * d->seq;
+    const int64_t ldkv = kv_row_stride ? kv_row_stride : 2 * W;
+    if (kv_row_stride < 0 || ldkv < 2 * W)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_cross_attn_sublayer: kv row stride below 2W");
+    if (M == 0) return SDXL_STATUS_OK;
+    if (workspace == nullptr || workspace_bytes < sdxl_cross_attn_sublayer_workspace_bytes(d) ||
+        !aligned(workspace, 256))
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT,
+                             "sdxl_cross_attn_sublayer: workspace missing, small or misaligned");
+    if (d->ctx_len > 0 && kv == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_cross_attn_sublayer: null tensor pointer");
+    char* ws = static_cast<char*>(workspace);
+    void* hidden_ws = ws;                               // [M, W]: LN output, later attention output
+    void* q = ws + (size_t)M * (size_t)W * 2;           // [M, W]
+    uint8_t* codes = static_cast<uint8_t*>(hidden_ws);  // E4M3 activations: codes, then row scales
+    float* code_scale = reinterpret_cast<float*>(ws + (size_t)M * (size_t)W);
+
+    sdxl_linear_desc qd{};
+    qd.m = M;
+    qd.n = W;
+    qd.k = W;
+    qd.w_dtype = d->w_q_dtype;
+    sdxl_status st;
+    if (act_fp8) {
+        st = sdxl_layer_norm_e4m3(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, codes, 0, code_scale, stream);
+        if (st != SDXL_STATUS_OK) return st;
+        st = sdxl_linear_e4m3(&qd, codes, code_scale, w_q, w_q_scale, nullptr, nullptr, q, stream);
+    } else {
+        st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+        if (st != SDXL_STATUS_OK) return st;
+        st = sdxl_linear(&qd, hidden_ws, w_q, w_q_scale, nullptr, nullptr, q, stream);
+    }
+    if (st != SDXL_STATUS_OK) return st;
+
+    sdxl_attn_desc ad{};
+    ad.batch = d->batch;
+    ad.q_seq = d->seq;
+    ad.k_seq = d->ctx_len;
+    ad.heads = d->heads;
+    ad.head_dim = 64;
+    ad.k_row_stride = ad.v_row_stride = ldkv;
+    ad.dtype = SDXL_DTYPE_F16;
+    ad.backend = d->attn_backend;
+    const char* kv_c = static_cast<const char*>(kv);
+    st = sdxl_attn_fwd(&ad, q, kv_c, kv_c == nullptr ? nullptr : kv_c + W * 2, nullptr, hidden_ws, stream);
     if (st != SDXL_STATUS_OK) return st;
 
     sdxl_linear_desc od{};

@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "sdxl_quantize_e4m3_rows",
     "sdxl_attn_sublayer_workspace_bytes",
     "sdxl_attn_sublayer",
+    "sdxl_cross_attn_sublayer_workspace_bytes",
+    "sdxl_cross_attn_sublayer",
 )
 
 
@@ -74,6 +76,14 @@ class SublayerDesc(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("seq", ctypes.c_int64), ("heads", ctypes.c_int64),
                 ("w_qkv_dtype", ctypes.c_int32), ("attn_backend", ctypes.c_int32),
                 ("ln_eps", ctypes.c_float), ("qkv_activations", ctypes.c_int32)]
+
+
+class CrossSublayerDesc(ctypes.Structure):
+    """Mirror of struct sdxl_cross_sublayer_desc."""
+
+    _fields_ = [("batch", ctypes.c_int64), ("seq", ctypes.c_int64), ("heads", ctypes.c_int64),
+                ("ctx_len", ctypes.c_int64), ("w_q_dtype", ctypes.c_int32), ("attn_backend", ctypes.c_int32),
+                ("ln_eps", ctypes.c_float), ("q_activations", ctypes.c_int32)]
 
 
 class SdxlError(RuntimeError):
@@ -129,6 +139,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sdxl_attn_sublayer.restype = ctypes.c_int
     lib.sdxl_attn_sublayer.argtypes = [ctypes.POINTER(SublayerDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                        ctypes.c_size_t, vp]
+    lib.sdxl_cross_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
+    lib.sdxl_cross_attn_sublayer_workspace_bytes.argtypes = [ctypes.POINTER(CrossSublayerDesc)]
+    lib.sdxl_cross_attn_sublayer.restype = ctypes.c_int
+    lib.sdxl_cross_attn_sublayer.argtypes = [ctypes.POINTER(CrossSublayerDesc), vp, vp, vp, vp, vp, vp, i64, vp, vp,
+                                             vp, vp, ctypes.c_size_t, vp]
     _LIB = lib
     return lib
 
@@ -329,6 +344,34 @@ def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads:
     _check(load().sdxl_attn_sublayer(ctypes.byref(d), _ptr(x), _ptr(ln_gamma), _ptr(ln_beta), _ptr(w_qkv),
                                      _ptr(w_qkv_scale), _ptr(w_out), _ptr(b_out), _ptr(out), _ptr(workspace),
                                      workspace.numel(), _stream(x)))
+    return out
+
+
+def project_context_kv(context, w_kv, w_kv_scale=None):
+    """K | V of the cross-attention context, once per request: context [B, L, C] fp16 against the
+    row-concatenated [to_k; to_v] weight [2W, C] (fp16, or uint8 E4M3 with w_kv_scale) -> [B, L, 2W]."""
+    B, L, C = context.shape
+    return linear(context.reshape(B * L, C), w_kv, w_scale=w_kv_scale).view(B, L, -1)
+
+
+def cross_attn_sublayer(x, ln_gamma, ln_beta, w_q, w_q_scale, kv, w_out, b_out, heads: int, out=None,
+                        workspace=None, backend: int = AUTO, eps: float = 0.0, fp8_activations: bool = False):
+    """x + to_out(attention(LN(x) . w_q^T, K, V)) for hidden x [B, S, W] fp16 with the context's
+    K | V in kv [B, L, 2W] (project_context_kv), the cross-attention half of the reference's
+    transformer block (src/cuda/unet.cpp:120-131)."""
+    import torch
+    B, S, W = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    d = CrossSublayerDesc(batch=B, seq=S, heads=heads, ctx_len=kv.shape[1],
+                          w_q_dtype=E4M3 if w_q.dtype == torch.uint8 else F16, attn_backend=backend, ln_eps=eps,
+                          q_activations=E4M3 if fp8_activations else F16)
+    nbytes = int(load().sdxl_cross_attn_sublayer_workspace_bytes(ctypes.byref(d)))
+    if workspace is None:
+        workspace = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)
+    _check(load().sdxl_cross_attn_sublayer(ctypes.byref(d), _ptr(x), _ptr(ln_gamma), _ptr(ln_beta), _ptr(w_q),
+                                           _ptr(w_q_scale), _ptr(kv), kv.stride(1), _ptr(w_out), _ptr(b_out),
+                                           _ptr(out), _ptr(workspace), workspace.numel(), _stream(x)))
     return out
 
 

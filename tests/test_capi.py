@@ -196,3 +196,23 @@ def test_sublayer_workspace_and_validation():
     assert L.sdxl_attn_sublayer(ctypes.byref(d), *args, 16, 256, 1 << 20, None) == sh.UNSUPPORTED
     assert L.sdxl_quantize_e4m3_rows(-1, 4, 16, 16, 16, None) == sh.INVALID_SHAPE
     assert L.sdxl_quantize_e4m3_rows(0, 4, 0, 0, 0, None) == sh.OK
+
+
+def test_cross_sublayer_workspace_and_validation():
+    import ctypes
+    d = sh.CrossSublayerDesc(batch=2, seq=1024, heads=20, ctx_len=77)
+    assert sh.load().sdxl_cross_attn_sublayer_workspace_bytes(ctypes.byref(d)) == 2 * 1024 * 1280 * 4
+    L = sh.load()
+    d = sh.CrossSublayerDesc(batch=2, seq=64, heads=2, ctx_len=77)
+    args = [16] * 6
+    assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 0, 16, 16, 16, None, 1 << 20, None) == \
+        sh.INVALID_ARGUMENT  # no workspace
+    assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 1, 16, 16, 16, 256, 1 << 20, None) == \
+        sh.INVALID_SHAPE  # kv row stride below 2W
+    d.q_activations = sh.E4M3  # E4M3 activations with fp16 w_q
+    assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 0, 16, 16, 16, 256, 1 << 20, None) == sh.UNSUPPORTED
+    d.q_activations = 9
+    assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 0, 16, 16, 16, 256, 1 << 20, None) == \
+        sh.INVALID_ARGUMENT
+    d = sh.CrossSublayerDesc(batch=0, seq=64, heads=2, ctx_len=77)
+    assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 0, 16, 16, 16, None, 0, None) == sh.OK  # empty
