@@ -1088,17 +1088,19 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
         }
     }
     const bool mask_all = p.causal || p.key_mask != nullptr;
-    // Mixed 12-wave workgroups (10 row blocks each, one per CU) when they fit
-    // one round and carry at most 10% more blocks per CU than an even share:
+    // Mixed 12-wave workgroups (10 row blocks each, one per CU at a time) when
+    // their rounds carry at most 10% more blocks per CU than an even share:
     // per SIMD 2.5 blocks with one K/V staging per 10 blocks. Measured against
     // the 4-wave grids in one process: [2,10,4096] 92.5 vs 94.0 us (exact
-    // fit), [4,20,960] 26.5 vs 29.5 us (240 of 256 CUs busy).
+    // fit), [4,20,960] 26.5 vs 29.5 us (240 of 256 CUs busy), [4,10,3840]
+    // 157.9 vs 169.9 us (two rounds, 480 workgroups).
     if (compute_units > 0 && !mask_all && p.k_seq % 64 == 0 && p.k_seq > 0) {
         const int64_t qb32 = (p.q_seq + 31) / 32;
         const int64_t total = qb32 * p.heads * p.batch;
         const int64_t wgs = (total + kMixedBlocks - 1) / kMixedBlocks;
-        if (qb32 >= kMixedBlocks && wgs <= compute_units &&
-            (double)kMixedBlocks <= 1.10 * (double)total / (double)compute_units) {
+        const int64_t rounds = (wgs + compute_units - 1) / compute_units;
+        if (qb32 >= kMixedBlocks && wgs <= INT32_MAX &&
+            (double)(rounds * kMixedBlocks) <= 1.10 * (double)total / (double)compute_units) {
             p.q_blocks = (int32_t)qb32;
             p.mixed_total = (int32_t)total;
             p.mixed_wgs = (int32_t)wgs;

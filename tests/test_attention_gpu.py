@@ -374,10 +374,10 @@ def test_short_keys_bf16():
 
 
 # ---------------------------------------------------------------- mixed 12-wave workgroups
-# Unmasked, non-causal calls with Sk % 64 == 0 whose 32-row blocks fill one round of 10-block
-# workgroups on the device within 10 % of an even share (T blocks with 2328 <= T <= 2560 on the
-# MI355X's 256 CUs, e.g. the north-star configs[2] and configs[4]'s level-2 self-attention) run one
-# 12-wave workgroup per CU: 8 waves with one row block each over
+# Unmasked, non-causal calls with Sk % 64 == 0 whose 32-row blocks fill rounds of 10-block
+# workgroups within 10 % of an even share per CU (T blocks, r rounds: r * 10 <= 1.1 * T / 256 on the
+# MI355X's 256 CUs, e.g. the north-star configs[2] and configs[4]'s self-attention at both levels)
+# run 12-wave workgroups, one per CU at a time: 8 waves with one row block each over
 # all keys and 2 row blocks split by 32-key group, merged through LDS. Workgroups may straddle
 # two heads and the last one may be short.
 
