@@ -268,26 +268,47 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 for (int j = 0; j < 2; ++j) acc[j][i] = mfma32_fp8(wop8[j], aop8[i], acc[j][i]);
             continue;
         }
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            i16x8 aop[kTM], wop[2];
+        // Operands of K step ks + 1 are read from LDS while step ks's MFMAs run
+        // (two register sets), so the LDS latency is not exposed at one or two
+        // waves per SIMD. E4M3 weights are read as codes and decoded just
+        // before their step.
+        i16x8 aop[2][kTM];
+        u32x4 wraw[2][2];  // fp16: the operand; E4M3: codes in the first two dwords
+        auto read_ops = [&](int ks, i16x8 (&a)[kTM], u32x4 (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if constexpr (kWFp8) {
                     const u32x2 raw = *(const lds_u32x2*)(wb + w_off[t] + ((ks ^ w_swz[t]) << 4));
-                    const uint2 lo = e4m3x4_to_f16(raw[0]), hi = e4m3x4_to_f16(raw[1]);
-                    wop[t] = __builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                    w[t] = u32x4{raw[0], raw[1], 0u, 0u};
                 } else {
-                    wop[t] = *(const lds_i16x8*)(wb + w_off[t] + (((2 * ks + hf) ^ w_swz[t]) << 4));
+                    w[t] = __builtin_bit_cast(u32x4, *(const lds_i16x8*)(wb + w_off[t] + (((2 * ks + hf) ^ w_swz[t]) << 4)));
                 }
             }
 #pragma unroll
             for (int t = 0; t < kTM; ++t)
-                aop[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
+                a[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
+        };
+        read_ops(0, aop[0], wraw[0]);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int cur = ks & 1;
+            if (ks < 3) read_ops(ks + 1, aop[cur ^ 1], wraw[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);  // keep the next step's reads ahead of this step's MFMAs
+            i16x8 wop[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                if constexpr (kWFp8) {
+                    const uint2 lo = e4m3x4_to_f16(wraw[cur][t][0]), hi = e4m3x4_to_f16(wraw[cur][t][1]);
+                    wop[t] = __builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                } else {
+                    wop[t] = __builtin_bit_cast(i16x8, wraw[cur][t]);
+                }
+            }
 #pragma unroll
             for (int i = 0; i < kTM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[j][i] = mfma32(wop[j], aop[i], acc[j][i]);
+                for (int j = 0; j < 2; ++j) acc[j][i] = mfma32(wop[j], aop[cur][i], acc[j][i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
