@@ -482,6 +482,63 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     }
 }
 
+// LayerNorm (fp16 output) for widths that are a multiple of 8 with 16-byte
+// aligned rows: lane l holds chunks l, l + 64, .. of 8 values (16-byte loads
+// and stores), otherwise as layer_norm_kernel (same two-pass centred variance,
+// fp32 maths, one rounding). kChunks = ceil(width / 512).
+typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
+template <int kChunks>
+__global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.rows) return;  // wave-uniform; no barrier in this kernel
+    const int chunks = p.width / 8;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + row * p.ldx);
+    f16x8v h[kChunks];
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) h[j] = x[min(lane + 64 * j, chunks - 1)];
+    float v[8 * kChunks];
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+        const bool ok = lane + 64 * j < chunks;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[8 * j + e] = ok ? (float)h[j][e] : 0.0f;
+            sum += v[8 * j + e];
+        }
+    }
+    const float inv_w = 1.0f / (float)p.width;
+    const float mean = wave_sum(sum) * inv_w;
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+        if (lane + 64 * j < chunks) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = v[8 * j + e] - mean;
+                sq += d * d;
+            }
+        }
+    }
+    const float var = fmaxf(wave_sum(sq) * inv_w, 0.0f);
+    const float inv = 1.0f / sqrtf(var + p.eps);
+    const f16x8v* g = (const f16x8v*)p.gamma;
+    const f16x8v* bt = (const f16x8v*)p.beta;
+    f16x8v* y = (f16x8v*)((_Float16*)p.y + row * p.ldy);
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) {
+        const int c = lane + 64 * j;
+        if (c < chunks) {
+            const f16x8v gg = g[c], bb = bt[c];
+            f16x8v o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (_Float16)((v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e]);
+            y[c] = o;
+        }
+    }
+}
+
 // Per-row E4M3 quantization of an fp16 weight [rows, cols] (reference
 // src/cuda/weights.cu:119-170): amax over the finite values of the row, scale
 // = amax > 0 ? max(amax / 448, 1e-12) : 1, code = E4M3(w / scale) rounded to
@@ -552,6 +609,21 @@ hipError_t launch_layer_norm(const LayerNormParams& p, hipStream_t stream) {
     if (p.width % 2 != 0 || p.width <= 0 || p.width > 128 * kLnMaxPer) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
     const bool e4m3 = p.y_scale != nullptr;
+    // 16-byte form for fp16 output: width % 8 == 0, 16-byte aligned rows
+    // (measured: [2048, 1280] 4.9 -> 4.0 us; [8192, 640] unchanged). The E4M3
+    // form stays on the pair kernel: its correctly rounded divisions run for
+    // every lane of a partly used 8-wide chunk (width 640: 9.7 vs 7.7 us).
+    const bool v8 = !e4m3 && p.width % 8 == 0 && p.ldx % 8 == 0 && p.ldy % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+                    ((uintptr_t)p.y & 15) == 0 && ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0;
+    if (v8) {
+        switch ((p.width + 511) / 512) {
+        case 1: hipLaunchKernelGGL((layer_norm_v8_kernel<1>), grid, block, 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((layer_norm_v8_kernel<2>), grid, block, 0, stream, p); break;
+        case 3: hipLaunchKernelGGL((layer_norm_v8_kernel<3>), grid, block, 0, stream, p); break;
+        default: hipLaunchKernelGGL((layer_norm_v8_kernel<4>), grid, block, 0, stream, p); break;
+        }
+        return hipGetLastError();
+    }
     switch ((p.width + 127) / 128) {
 #define SDXL_LN_CASE(n)                                                                   \
     case n:                                                                               \
