@@ -168,6 +168,8 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
 
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
 
+__device__ __forceinline__ void wait_vmem4() { __builtin_amdgcn_s_waitcnt(0x0074); }     // vmcnt(4)
+
 // Workgroup kinds of the fused kernel.
 constexpr int kKindWhole = 0;  // 4 waves: 128 query rows, all keys
 constexpr int kKindSplit = 1;  // 4 waves: 64 query rows, each row block's keys in two halves
@@ -803,21 +805,32 @@ __global__ __launch_bounds__(12 * 64, 3) void fused_attention_d64_mixed_kernel(F
 // in LDS once, then each wave walks its blocks (w, w + kWaves, ...) computing
 // the exact softmax in one pass (no running anchor, no rescaling):
 // S^T = K Q^T for all key groups, one maximum, exp2, one sum, O^T = V^T P^T.
-// The Q operands of a wave's next block are loaded before the current block
-// is computed, so HBM reads overlap the matrix/VALU work and the stores.
-// The VALU work per block is kept small (about one wave per SIMD leaves no
-// latency hiding): Q is used as stored and the scale is folded into one fma
-// per exp2 argument; only the last key group is bounds-checked.
+// A wave's block is one dependent chain (Q -> scores -> max -> exp2 -> PV ->
+// output) of about 1.5 us, so throughput comes from residency: the kernel
+// keeps ~110 VGPRs and 40 KiB of LDS per 4-wave workgroup (3 key groups) so
+// that four waves share each SIMD. The next block's Q rows are transferred
+// into the wave's LDS buffer as soon as the current block's output has left
+// it for registers, overlapping that block's stores.
+// Q is used as stored and the scale is folded into one fma per exp2
+// argument. Keys past k_seq get a -inf accumulator seed in the last group;
+// when that group holds at most 16 keys (kHalf, e.g. 77 = 64 + 13) its upper
+// half is skipped in the exponentials and in PV.
 // kGroups = ceil(k_seq / 32). Visibility per key: key < k_seq, key mask,
 // causal (key <= query); a row with no visible key is 0 (reference
 // src/cuda/flash_attention_sm80.cu:214-219).
-template <bool IsBf16, int kGroups, bool kMasked, int kWaves>
-__global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kernel(FusedAttentionParams p) {
+// Workgroups per CU: LDS takes 16 + 8 groups KiB per workgroup; 96 keys
+// without the half group need more than 128 VGPRs.
+constexpr int short_keys_occupancy(int groups, bool half) { return groups == 4 || (groups == 3 && !half) ? 3 : 4; }
+
+template <bool IsBf16, int kGroups, bool kHalf, bool kMasked, int kWaves>
+__global__ __launch_bounds__(kWaves * 64, short_keys_occupancy(kGroups, kHalf)) void short_keys_attention_d64_kernel(FusedAttentionParams p) {
     constexpr int kRows = 32 * kGroups;
+    constexpr int kLastN = kHalf ? 8 : 16;  // elements of the last group's scores in use (kHalf: keys 0-15 of it)
     constexpr int kPerWave = 8 * kGroups / kWaves;  // 1-KiB transfers per wave (4 kGroups for K, 4 kGroups for V)
+    constexpr int kBlockBytes = 32 * kRowBytes;
     __shared__ __attribute__((aligned(16))) char kbuf[kRows * kRowBytes];
     __shared__ __attribute__((aligned(16))) char vbuf[kRows * kRowBytes];
-    __shared__ __attribute__((aligned(16))) char qobuf[kWaves * 32 * kRowBytes];  // per-wave Q / O staging
+    __shared__ __attribute__((aligned(16))) char qobuf[kWaves * kBlockBytes];  // per-wave Q / O staging
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -857,22 +870,27 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
         lds_dma16(is_v ? vbase : kbase, off, lds_addr((is_v ? vbuf : kbuf) + 8 * r8 * kRowBytes));
     }
 
-    // Q rows move HBM -> registers -> a wave-private LDS buffer in whole
-    // 128-byte row segments (8 lanes per row, 16 B each: coalesced), and the
-    // output leaves the same way; rows are stored swizzled as the K tiles.
-    // qraw[j]: row 8j + lane / 8 of the block, 16-byte chunk lane % 8.
-    auto load_q_rows = [&](int first_row, u32x4 (&qraw)[4]) __attribute__((always_inline)) {
+    // Q rows move HBM -> LDS by DMA into the wave's block buffer (whole
+    // 128-byte row segments, 8 lanes per row: coalesced), stored swizzled as
+    // the K tiles; rows past q_seq re-read the last row and are never stored.
+    // The output leaves through the same buffer. A wave's blocks are
+    // blk_begin + wave + kWaves i, i < n_mine.
+    char* const wbuf = qobuf + wave * kBlockBytes;
+    const int first = blk_begin + wave;
+    const int n_mine = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
+    const uint32_t q_stride_b = (uint32_t)(p.q_row_stride * elem);
+    auto issue_q = [&](int i) __attribute__((always_inline)) {
+        const int blk = first + kWaves * i;
+        const char* src = qbase + (int64_t)(32 * blk) * p.q_row_stride * elem;
+        const int last = p.q_seq - 1 - 32 * blk;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int row = first_row + 8 * j + (lane >> 3);
-            qraw[j] = row < p.q_seq ? *(const u32x4*)(qbase + (int64_t)row * p.q_row_stride * elem + 16 * (lane & 7))
-                                    : u32x4{0, 0, 0, 0};
+            const int row = 8 * j + (lane >> 3);
+            const uint32_t off = __umul24((uint32_t)min(row, last), q_stride_b) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            lds_dma16(src, off, lds_addr(wbuf + 8 * j * kRowBytes));
         }
     };
-    char* wbuf = qobuf + wave * (32 * kRowBytes);
-    int blk = blk_begin + wave;
-    u32x4 qnext[4];
-    load_q_rows(32 * blk, qnext);
+    if (n_mine > 0) issue_q(0);
     // Visibility words of keys lane and lane + 64 (wave-uniform ballots):
     // key < k_seq and, with a key mask, mask != 0.
     uint64_t vis_word[2] = {~0ull, ~0ull};
@@ -884,7 +902,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
             vis_word[w] = __builtin_amdgcn_ballot_w64(ok);
         }
     }
-    wait_vmem_all();
+    // K and V landed (block 0's Q, issued after them, may still fly)
+    if (n_mine > 0) wait_vmem4();
+    else wait_vmem_all();
     __syncthreads();
 
     const int k_swz = swz(col);
@@ -899,19 +919,25 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
             v_off[dt][hi] = (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) + ((tr_qd & 1) << 3);
     }
     const float c = p.scale_log2;
-
-    for (; blk < blk_end; blk += kWaves) {
-        const int my_query = 32 * blk + col;
-        // park this block's Q rows, start the next block's loads (in flight
-        // during this block), read the Q^T operand: lane holds dims
-        // 16ks + 8hf .. +7 of query row col (used as stored: the softmax scale
-        // is applied in fp32 to the scores, folded into the exp2 argument).
+    // Accumulator seed of the last key group: -inf for keys past k_seq, so
+    // that the scores of those keys come out of the MFMA as -inf.
+    f32x16 seed_last;
+    {
+        const int lim = p.k_seq - 32 * (kGroups - 1) - 4 * hf;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = 8 * j + (lane >> 3);
-            *(lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4)) = qnext[j];
-        }
-        if (blk + kWaves < blk_end) load_q_rows(32 * (blk + kWaves), qnext);
+        for (int i = 0; i < 16; ++i) seed_last[i] = 8 * (i >> 2) + (i & 3) < lim ? 0.0f : -__builtin_inff();
+    }
+
+    for (int i = 0; i < n_mine; ++i) {
+        const int blk = first + kWaves * i;
+        const int my_query = 32 * blk + col;
+        // Block i's transfer was issued before block i - 1's 4 stores (and
+        // block 0's after K and V).
+        if (i == 0) wait_vmem_all();
+        else wait_vmem4();
+        // Q^T operand: lane holds dims 16ks + 8hf .. +7 of query row col (used
+        // as stored: the softmax scale is applied in fp32 to the scores, folded
+        // into the exp2 argument).
         i16x8 qop[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qop[ks] = *(const lds_i16x8*)(wbuf + col * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
@@ -928,7 +954,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
             f32x16 z;
 #pragma unroll
             for (int i = 0; i < 16; ++i) z[i] = 0.0f;
-            s[g] = mfma32<IsBf16>(k_operand(g, 0), qop[0], z);
+            s[g] = mfma32<IsBf16>(k_operand(g, 0), qop[0], g == kGroups - 1 ? seed_last : z);
         }
 #pragma unroll
         for (int ks = 1; ks < 4; ++ks)
@@ -947,18 +973,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
                     s[g][i] = ok ? s[g][i] : -__builtin_inff();
                 }
             }
-        } else if (p.k_seq % 32 != 0) {
-            // only the last group can hold keys past k_seq
-            const int lim = p.k_seq - 32 * (kGroups - 1) - 4 * hf;
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                s[kGroups - 1][i] = 8 * (i >> 2) + (i & 3) < lim ? s[kGroups - 1][i] : -__builtin_inff();
         }
         float mx = -__builtin_inff();
 #pragma unroll
         for (int g = 0; g < kGroups; ++g)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[g][i]);
+            for (int i = 0; i < (g == kGroups - 1 ? kLastN : 16); ++i) mx = fmaxf(mx, s[g][i]);
         mx = xhalf_max(mx);
         // p = 2^(c s - c max), c = scale log2(e); no visible key: every p is 0
         const float neg_cm = mx == -__builtin_inff() ? 0.0f : -c * mx;
@@ -973,12 +993,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
         float l = 0.0f;
 #pragma unroll
         for (int g = 0; g < kGroups; ++g) {
+            // kHalf: keys 16-31 of the last group are all past k_seq; their
+            // probabilities and PV step are skipped.
+            constexpr int kSteps = 2;
+            const int n_ss = (kHalf && g == kGroups - 1) ? 1 : kSteps;
             float e[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c, neg_cm));
-            l += sum8(e) + sum8(e + 8);
+            for (int i = 0; i < 16; ++i)
+                e[i] = i < 8 * n_ss ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c, neg_cm)) : 0.0f;
+            l += n_ss == 2 ? sum8(e) + sum8(e + 8) : sum8(e);
 #pragma unroll
-            for (int ss = 0; ss < 2; ++ss) {
+            for (int ss = 0; ss < n_ss; ++ss) {
                 const i16x8 pop = __builtin_bit_cast(
                     i16x8, u32x4{pack2<IsBf16>(e[8 * ss], e[8 * ss + 1]), pack2<IsBf16>(e[8 * ss + 2], e[8 * ss + 3]),
                                  pack2<IsBf16>(e[8 * ss + 4], e[8 * ss + 5]), pack2<IsBf16>(e[8 * ss + 6], e[8 * ss + 7])});
@@ -1004,26 +1029,40 @@ __global__ __launch_bounds__(kWaves * 64, 2) void short_keys_attention_d64_kerne
                 const uint32_t w1 = pack2<IsBf16>(out[dt][4 * u + 2] * inv, out[dt][4 * u + 3] * inv);
                 *(lds_u32x2*)(wbuf + col * kRowBytes + (((4 * dt + u) ^ k_swz) << 4) + 8 * hf) = u32x2{w0, w1};
             }
+        u32x4 orow[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = 8 * j + (lane >> 3);
-            const u32x4 w = *(const lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+            orow[j] = *(const lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+        }
+        // the buffer is free once its output rows are in registers
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (i + 1 < n_mine) issue_q(i + 1);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3);
             if (32 * blk + row < p.q_seq)
-                *(u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)) = w;
+                *(u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)) = orow[j];
         }
     }
 }
 
-template <bool IsBf16, bool kMasked, int kWaves>
-hipError_t launch_short_keys_w(FusedAttentionParams p, int compute_units, hipStream_t stream) {
-    // Chunks: about two workgroups per CU in total (measured best of 1-8 on
-    // the 77-token shapes), each a run of consecutive 32-row blocks of one
-    // head, a whole number of blocks per wave (longer chunks amortise the K/V
-    // staging and let each wave prefetch its next block).
+template <bool IsBf16, bool kMasked>
+hipError_t launch_short_keys(FusedAttentionParams p, int compute_units, hipStream_t stream) {
+    // Chunks: about as many workgroups as fit on the device at once (four per
+    // CU, or three), each a run of consecutive 32-row
+    // blocks of one head, a whole number of blocks per wave. Measured on the
+    // 77-token shapes against 1-3 per CU and fixed chunks of 4-12 blocks:
+    // [2,10,4096] 8.4 -> 7.2 us, [4,20,960] 8.3 -> 7.0 us at two per CU.
+    constexpr int kWaves = 4;
+    const int groups = (p.k_seq + 31) / 32;
+    // kHalf when the last 32-key group holds at most 16 keys
+    const bool half = (p.k_seq - 1) % 32 < 16;
+    const int per_cu = short_keys_occupancy(groups, half);
     p.q_blocks = (p.q_seq + 31) / 32;
     const int64_t heads_total = (int64_t)p.heads * p.batch;
     const int64_t all_blocks = (int64_t)p.q_blocks * heads_total;
-    const int64_t target_wgs = (int64_t)(compute_units > 0 ? compute_units : 256) * 2;
+    const int64_t target_wgs = (int64_t)(compute_units > 0 ? compute_units : 256) * per_cu;
     int64_t chunk = (all_blocks + target_wgs - 1) / target_wgs;
     chunk = (chunk + kWaves - 1) / kWaves * kWaves;  // whole rounds of the workgroup's waves
     chunk = chunk > p.q_blocks ? p.q_blocks : chunk;
@@ -1033,18 +1072,16 @@ hipError_t launch_short_keys_w(FusedAttentionParams p, int compute_units, hipStr
     if (grid_size > INT32_MAX) return hipErrorInvalidValue;
     p.total_blocks = (int32_t)grid_size;
     const dim3 grid(p.total_blocks), block(64 * kWaves);
-    switch ((p.k_seq + 31) / 32) {
-    case 1: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 1, kMasked, kWaves>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 2, kMasked, kWaves>), grid, block, 0, stream, p); break;
-    case 3: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 3, kMasked, kWaves>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, 4, kMasked, kWaves>), grid, block, 0, stream, p); break;
+#define SDXL_SK_LAUNCH(G, H) \
+    hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, G, H, kMasked, kWaves>), grid, block, 0, stream, p)
+    switch (groups) {
+    case 1: if (half) SDXL_SK_LAUNCH(1, true); else SDXL_SK_LAUNCH(1, false); break;
+    case 2: if (half) SDXL_SK_LAUNCH(2, true); else SDXL_SK_LAUNCH(2, false); break;
+    case 3: if (half) SDXL_SK_LAUNCH(3, true); else SDXL_SK_LAUNCH(3, false); break;
+    default: if (half) SDXL_SK_LAUNCH(4, true); else SDXL_SK_LAUNCH(4, false); break;
     }
+#undef SDXL_SK_LAUNCH
     return hipGetLastError();
-}
-
-template <bool IsBf16, bool kMasked>
-hipError_t launch_short_keys(const FusedAttentionParams& p, int compute_units, hipStream_t stream) {
-    return launch_short_keys_w<IsBf16, kMasked, 4>(p, compute_units, stream);
 }
 
 }  // namespace

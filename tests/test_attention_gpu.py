@@ -324,9 +324,16 @@ def test_key_split_workgroups(B, Sq, Sk, H):
 # One-pass kernel with K/V wholly in LDS: the 77-token cross-attention and CLIP's causal
 # self-attention (src/cuda/text_encoder.cpp:83, 77 tokens).
 
-@pytest.mark.parametrize("sk", [1, 2, 31, 32, 33, 64, 77, 96, 127, 128])
+@pytest.mark.parametrize("sk", [1, 2, 16, 17, 31, 32, 33, 48, 49, 64, 77, 80, 81, 96, 112, 127, 128])
 def test_short_keys_lengths(sk):
     _check_config(2, 200, sk, 3, seed=900 + sk)
+
+
+@pytest.mark.parametrize("sq", [8192, 8190])
+def test_short_keys_several_blocks_per_wave(sq):
+    """Long query sequences: each wave walks several 32-row blocks of its chunk, the Q rows of
+    the next block in flight while the current one is computed (ragged last block at 8190)."""
+    _check_config(2, sq, 77, 10, seed=950 + sq % 7)
 
 
 @pytest.mark.parametrize("causal", [False, True])
