@@ -176,6 +176,11 @@ constexpr int kKindSplit = 1;  // 4 waves: 64 query rows, each row block's keys 
 constexpr int kKindMixed = 2;  // 12 waves: 10 consecutive 32-row blocks, 8 whole + 2 split in groups
 constexpr int kMixedFull = 8;    // waves of a mixed workgroup that take one row block and all keys
 constexpr int kMixedBlocks = 10; // 32-row blocks per mixed workgroup
+// Output staging after the key loop (merge slots, then 4 KiB per storing
+// wave) fits in the stage buffers of each kind.
+static_assert(2 * 34 * 64 * 4 + 2 * 32 * kRowBytes <= (kKRing + kVRing) * kTileBytes, "key-split epilogue staging");
+static_assert(4 * 32 * kRowBytes <= (kKRing + kVRing) * kTileBytes, "whole epilogue staging");
+static_assert(2 * 34 * 64 * 4 + (kMixedFull + 2) * 32 * kRowBytes <= 2 * (kKRing + kVRing) * kTileBytes, "mixed epilogue staging");
 
 // The kernel body for one workgroup kind.
 template <int kWaves, bool IsBf16, bool kMaskAll, int kKind>
@@ -757,21 +762,35 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         }
     }
 
-    // ---- epilogue: normalise, convert, store. Lane holds, for d-tile dt,
-    // dims 32dt + 8u + 4hf + (0..3) of its query in acc[dt][4u .. 4u+3].
+    // ---- epilogue: normalise, convert, and write the wave's 32 output rows
+    // to LDS (a wave-private 4 KiB buffer past the merge slots, 16-byte
+    // chunks XOR-swizzled by row as the K tiles), then store whole 128-byte
+    // row segments (8 lanes per row) with non-temporal stores. Lane holds,
+    // for d-tile dt, dims 32dt + 8u + 4hf + (0..3) of its query in
+    // acc[dt][4u .. 4u+3], i.e. half hf of 16-byte chunk 4dt + u.
+    if constexpr (!split && !mixed) __syncthreads();  // every wave is done with the stage buffers
     const float l_tot = xhalf_sum(l_run);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (active && my_query < p.q_seq) {
-        char* orow = obase + (int64_t)my_query * p.o_row_stride * elem;
+    if (active) {
+        constexpr int kParkBytes = 2 * 34 * 64 * 4;  // merge slots (split and mixed kinds)
+        const int stage = mixed ? (half_wave ? kMixedFull + ((wave - kMixedFull) >> 1) : wave) : split ? (wave & 1) : wave;
+        char* sbuf = &ring[0][0] + ((split || mixed) ? kParkBytes : 0) + stage * (32 * kRowBytes);
+        const int sw = swz(col);
 #pragma unroll
         for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint32_t w0 = pack2<IsBf16>(acc[dt][4 * u] * inv, acc[dt][4 * u + 1] * inv);
                 const uint32_t w1 = pack2<IsBf16>(acc[dt][4 * u + 2] * inv, acc[dt][4 * u + 3] * inv);
-                const int d = 32 * dt + 8 * u + 4 * hf;
-                *(uint2*)(orow + d * 2) = uint2{w0, w1};
+                *(lds_u32x2*)(sbuf + col * kRowBytes + (((4 * dt + u) ^ sw) << 4) + 8 * hf) = u32x2{w0, w1};
             }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            const u32x4 w = *(const lds_u32x4*)(sbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+            if (q0 + row < p.q_seq)
+                __builtin_nontemporal_store(w, (u32x4*)(obase + (int64_t)(q0 + row) * p.o_row_stride * elem + 16 * (lane & 7)));
+        }
     }
 }
 
@@ -1038,11 +1057,14 @@ __global__ __launch_bounds__(kWaves * 64, short_keys_occupancy(kGroups, kHalf)) 
         // the buffer is free once its output rows are in registers
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (i + 1 < n_mine) issue_q(i + 1);
+        // Non-temporal stores: the output is not read again by this kernel,
+        // and whole 128-byte row segments per 8 lanes stream out without
+        // occupying L2 (measured [4,10,3840,77] 11.4 -> 9.8 us).
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = 8 * j + (lane >> 3);
             if (32 * blk + row < p.q_seq)
-                *(u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)) = orow[j];
+                __builtin_nontemporal_store(orow[j], (u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)));
         }
     }
 }
