@@ -361,8 +361,8 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                     const float v1 = a[1] * rs[it] * e_scale.y + e_bias.y + (float)res[it][1];
                     const float v2 = a[2] * rs[it] * e_scale.z + e_bias.z + (float)res[it][2];
                     const float v3 = a[3] * rs[it] * e_scale.w + e_bias.w + (float)res[it][3];
-                    *(f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en) =
-                        f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3};
+                    __builtin_nontemporal_store(f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3},
+                                                (f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en));
                 }
             }
         }
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
                 // y / scale correctly rounded, as the weight quantiser divides
                 const float q0 = fminf(fmaxf(yv[2 * j] / scale, -448.0f), 448.0f);
                 const float q1 = fminf(fmaxf(yv[2 * j + 1] / scale, -448.0f), 448.0f);
-                q[c] = (uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu);
+                __builtin_nontemporal_store((uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu), q + c);
             }
         }
         return;
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
             const f16x2 gg = g[c], bb = bt[c];
             const float y0 = (v[2 * j] - mean) * inv * (float)gg[0] + (float)bb[0];
             const float y1 = (v[2 * j + 1] - mean) * inv * (float)gg[1] + (float)bb[1];
-            y[c] = f16x2{(_Float16)y0, (_Float16)y1};
+            __builtin_nontemporal_store(f16x2{(_Float16)y0, (_Float16)y1}, y + c);
         }
     }
 }
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
             f16x8v o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = (_Float16)((v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e]);
-            y[c] = o;
+            __builtin_nontemporal_store(o, y + c);
         }
     }
 }
