@@ -170,6 +170,15 @@ __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0
 
 __device__ __forceinline__ void wait_vmem4() { __builtin_amdgcn_s_waitcnt(0x0074); }     // vmcnt(4)
 
+// Output store: non-temporal (streams to memory instead of staying in L2)
+// for large outputs, else ordinary. A compile-time choice: with a run-time
+// flag the compiler merges both branches into one ordinary store.
+template <bool kNt, typename T>
+__device__ __forceinline__ void store_out(T v, T* ptr) {
+    if constexpr (kNt) __builtin_nontemporal_store(v, ptr);
+    else *ptr = v;
+}
+
 // Workgroup kinds of the fused kernel.
 constexpr int kKindWhole = 0;  // 4 waves: 128 query rows, all keys
 constexpr int kKindSplit = 1;  // 4 waves: 64 query rows, each row block's keys in two halves
@@ -789,7 +798,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             const int row = 8 * j + (lane >> 3);
             const u32x4 w = *(const lds_u32x4*)(sbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
             if (q0 + row < p.q_seq)
-                __builtin_nontemporal_store(w, (u32x4*)(obase + (int64_t)(q0 + row) * p.o_row_stride * elem + 16 * (lane & 7)));
+                store_out<mixed>(w, (u32x4*)(obase + (int64_t)(q0 + row) * p.o_row_stride * elem + 16 * (lane & 7)));
         }
     }
 }
@@ -841,7 +850,7 @@ __global__ __launch_bounds__(12 * 64, 3) void fused_attention_d64_mixed_kernel(F
 // without the half group need more than 128 VGPRs.
 constexpr int short_keys_occupancy(int groups, bool half) { return groups == 4 || (groups == 3 && !half) ? 3 : 4; }
 
-template <bool IsBf16, int kGroups, bool kHalf, bool kMasked, int kWaves>
+template <bool IsBf16, int kGroups, bool kHalf, bool kMasked, int kWaves, bool kNt>
 __global__ __launch_bounds__(kWaves * 64, short_keys_occupancy(kGroups, kHalf)) void short_keys_attention_d64_kernel(FusedAttentionParams p) {
     constexpr int kRows = 32 * kGroups;
     constexpr int kLastN = kHalf ? 8 : 16;  // elements of the last group's scores in use (kHalf: keys 0-15 of it)
@@ -1057,14 +1066,13 @@ __global__ __launch_bounds__(kWaves * 64, short_keys_occupancy(kGroups, kHalf)) 
         // the buffer is free once its output rows are in registers
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (i + 1 < n_mine) issue_q(i + 1);
-        // Non-temporal stores: the output is not read again by this kernel,
-        // and whole 128-byte row segments per 8 lanes stream out without
-        // occupying L2 (measured [4,10,3840,77] 11.4 -> 9.8 us).
+        // Whole 128-byte row segments per 8 lanes; non-temporal for large
+        // outputs (measured [4,10,3840,77] 11.4 -> 9.8 us).
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = 8 * j + (lane >> 3);
             if (32 * blk + row < p.q_seq)
-                __builtin_nontemporal_store(orow[j], (u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)));
+                store_out<kNt>(orow[j], (u32x4*)(obase + (int64_t)(32 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)));
         }
     }
 }
@@ -1094,8 +1102,13 @@ hipError_t launch_short_keys(FusedAttentionParams p, int compute_units, hipStrea
     if (grid_size > INT32_MAX) return hipErrorInvalidValue;
     p.total_blocks = (int32_t)grid_size;
     const dim3 grid(p.total_blocks), block(64 * kWaves);
-#define SDXL_SK_LAUNCH(G, H) \
-    hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, G, H, kMasked, kWaves>), grid, block, 0, stream, p)
+    // non-temporal output stores for large outputs
+    const bool nt = (int64_t)p.batch * p.q_seq * p.heads * kHeadDim * 2 >= kStreamOutBytes;
+#define SDXL_SK_LAUNCH(G, H)                                                                                        \
+    do {                                                                                                            \
+        if (nt) hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, G, H, kMasked, kWaves, true>), grid, block, 0, stream, p); \
+        else hipLaunchKernelGGL((short_keys_attention_d64_kernel<IsBf16, G, H, kMasked, kWaves, false>), grid, block, 0, stream, p); \
+    } while (0)
     switch (groups) {
     case 1: if (half) SDXL_SK_LAUNCH(1, true); else SDXL_SK_LAUNCH(1, false); break;
     case 2: if (half) SDXL_SK_LAUNCH(2, true); else SDXL_SK_LAUNCH(2, false); break;

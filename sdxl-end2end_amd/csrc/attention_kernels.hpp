@@ -8,6 +8,11 @@ namespace sdxl_hip {
 
 // Waves per workgroup of the fused kernel (32 query rows per wave).
 constexpr int kFusedWaves = 4;
+// Outputs of at least this many bytes are written with non-temporal stores:
+// they stream to memory instead of occupying L2 (measured faster for the
+// 10-40 MB outputs of the level-1 shapes; smaller outputs, read back by the
+// next kernel of a sublayer, were faster with ordinary stores).
+constexpr int64_t kStreamOutBytes = int64_t{8} << 20;
 // Key sequences up to this length run the one-pass short-key kernel (K/V wholly in LDS).
 constexpr int kShortKeysMax = 128;
 

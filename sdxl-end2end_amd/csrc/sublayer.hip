@@ -92,6 +92,15 @@ __device__ __forceinline__ uint2 e4m3x4_to_f16(uint32_t x) {
 }
 
 // s_waitcnt vmcnt(n) (lgkmcnt(0), expcnt untouched) for a compile-time n < 64.
+// Output store: non-temporal (streams to memory instead of staying in L2)
+// for large outputs, else ordinary. A compile-time choice: with a run-time
+// flag the compiler merges both branches into one ordinary store.
+template <bool kNt, typename T>
+__device__ __forceinline__ void store_out(T v, T* ptr) {
+    if constexpr (kNt) __builtin_nontemporal_store(v, ptr);
+    else *ptr = v;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -114,7 +123,7 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 // (64-byte rows, chunk swizzle (row >> 2) & 3) and are decoded when the
 // operand is read; fp16 weights use the A-operand layout. kAFp8 (with kWFp8):
 // E4M3 activations in 64-byte rows, fp8 MFMA.
-template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc>
+template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt>
 __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
     constexpr int kBMt = 64 * kTM;
@@ -361,8 +370,8 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                     const float v1 = a[1] * rs[it] * e_scale.y + e_bias.y + (float)res[it][1];
                     const float v2 = a[2] * rs[it] * e_scale.z + e_bias.z + (float)res[it][2];
                     const float v3 = a[3] * rs[it] * e_scale.w + e_bias.w + (float)res[it][3];
-                    __builtin_nontemporal_store(f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3},
-                                                (f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en));
+                    store_out<kNt>(f16x4{(_Float16)v0, (_Float16)v1, (_Float16)v2, (_Float16)v3},
+                                   (f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en));
                 }
             }
         }
@@ -409,7 +418,7 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
-template <int kPer, bool kE4M3>
+template <int kPer, bool kE4M3, bool kNt>
 __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -464,7 +473,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
                 // y / scale correctly rounded, as the weight quantiser divides
                 const float q0 = fminf(fmaxf(yv[2 * j] / scale, -448.0f), 448.0f);
                 const float q1 = fminf(fmaxf(yv[2 * j + 1] / scale, -448.0f), 448.0f);
-                __builtin_nontemporal_store((uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu), q + c);
+                store_out<kNt>((uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu), q + c);
             }
         }
         return;
@@ -477,7 +486,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
             const f16x2 gg = g[c], bb = bt[c];
             const float y0 = (v[2 * j] - mean) * inv * (float)gg[0] + (float)bb[0];
             const float y1 = (v[2 * j + 1] - mean) * inv * (float)gg[1] + (float)bb[1];
-            __builtin_nontemporal_store(f16x2{(_Float16)y0, (_Float16)y1}, y + c);
+            store_out<kNt>(f16x2{(_Float16)y0, (_Float16)y1}, y + c);
         }
     }
 }
@@ -487,7 +496,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
 // and stores), otherwise as layer_norm_kernel (same two-pass centred variance,
 // fp32 maths, one rounding). kChunks = ceil(width / 512).
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-template <int kChunks>
+template <int kChunks, bool kNt>
 __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -534,7 +543,7 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
             f16x8v o;
 #pragma unroll
             for (int e = 0; e < 8; ++e) o[e] = (_Float16)((v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e]);
-            __builtin_nontemporal_store(o, y + c);
+            store_out<kNt>(o, y + c);
         }
     }
 }
@@ -589,26 +598,36 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
     const int64_t tasks = (int64_t)p.m_blocks * p.n_blocks;
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(256);
+    // non-temporal output stores for large outputs
+    const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;
+#define SDXL_LIN(WF, AF, TM, RING)                                                                              \
+    do {                                                                                                        \
+        if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, true>), grid, block, 0, stream, p);      \
+        else hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, false>), grid, block, 0, stream, p);        \
+    } while (0)
     if (a_fp8) {
-        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2>), grid, block, 0, stream, p);
-        else if (use_short) hipLaunchKernelGGL((linear_kernel<true, true, 1, 2, 2>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((linear_kernel<true, true, 2, 3, 2>), grid, block, 0, stream, p);
+        if (use_tall) SDXL_LIN(true, true, 4, 3);
+        else if (use_short) SDXL_LIN(true, true, 1, 2);
+        else SDXL_LIN(true, true, 2, 3);
     } else if (w_fp8) {
-        if (use_tall) hipLaunchKernelGGL((linear_kernel<true, false, 4, 2, 2>), grid, block, 0, stream, p);
-        else if (use_short) hipLaunchKernelGGL((linear_kernel<true, false, 1, 2, 2>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((linear_kernel<true, false, 2, 3, 2>), grid, block, 0, stream, p);
+        if (use_tall) SDXL_LIN(true, false, 4, 2);
+        else if (use_short) SDXL_LIN(true, false, 1, 2);
+        else SDXL_LIN(true, false, 2, 3);
     } else {
-        if (use_short) hipLaunchKernelGGL((linear_kernel<false, false, 1, 2, 2>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((linear_kernel<false, false, 2, 2, 2>), grid, block, 0, stream, p);
+        if (use_short) SDXL_LIN(false, false, 1, 2);
+        else SDXL_LIN(false, false, 2, 2);
     }
+#undef SDXL_LIN
     return hipGetLastError();
 }
 
-hipError_t launch_layer_norm(const LayerNormParams& p, hipStream_t stream) {
+hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t stream) {
+    LayerNormParams p = params_in;
     if (p.rows == 0) return hipSuccess;
     if (p.width % 2 != 0 || p.width <= 0 || p.width > 128 * kLnMaxPer) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
     const bool e4m3 = p.y_scale != nullptr;
+    const bool nt = p.rows * p.width * (e4m3 ? 1 : 2) >= kStreamOutBytes;  // non-temporal stores for large outputs
     // 16-byte form for fp16 output: width % 8 == 0, 16-byte aligned rows
     // (measured: [2048, 1280] 4.9 -> 4.0 us; [8192, 640] unchanged). The E4M3
     // form stays on the pair kernel: its correctly rounded divisions run for
@@ -617,18 +636,24 @@ hipError_t launch_layer_norm(const LayerNormParams& p, hipStream_t stream) {
                     ((uintptr_t)p.y & 15) == 0 && ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0;
     if (v8) {
         switch ((p.width + 511) / 512) {
-        case 1: hipLaunchKernelGGL((layer_norm_v8_kernel<1>), grid, block, 0, stream, p); break;
-        case 2: hipLaunchKernelGGL((layer_norm_v8_kernel<2>), grid, block, 0, stream, p); break;
-        case 3: hipLaunchKernelGGL((layer_norm_v8_kernel<3>), grid, block, 0, stream, p); break;
-        default: hipLaunchKernelGGL((layer_norm_v8_kernel<4>), grid, block, 0, stream, p); break;
+#define SDXL_LN8(n)                                                                                   \
+    if (nt) hipLaunchKernelGGL((layer_norm_v8_kernel<n, true>), grid, block, 0, stream, p);        \
+    else hipLaunchKernelGGL((layer_norm_v8_kernel<n, false>), grid, block, 0, stream, p);
+        case 1: SDXL_LN8(1) break;
+        case 2: SDXL_LN8(2) break;
+        case 3: SDXL_LN8(3) break;
+        default: SDXL_LN8(4) break;
+#undef SDXL_LN8
         }
         return hipGetLastError();
     }
     switch ((p.width + 127) / 128) {
 #define SDXL_LN_CASE(n)                                                                   \
     case n:                                                                               \
-        if (e4m3) hipLaunchKernelGGL((layer_norm_kernel<n, true>), grid, block, 0, stream, p); \
-        else hipLaunchKernelGGL((layer_norm_kernel<n, false>), grid, block, 0, stream, p);     \
+        if (e4m3 && nt) hipLaunchKernelGGL((layer_norm_kernel<n, true, true>), grid, block, 0, stream, p);   \
+        else if (e4m3) hipLaunchKernelGGL((layer_norm_kernel<n, true, false>), grid, block, 0, stream, p);   \
+        else if (nt) hipLaunchKernelGGL((layer_norm_kernel<n, false, true>), grid, block, 0, stream, p);     \
+        else hipLaunchKernelGGL((layer_norm_kernel<n, false, false>), grid, block, 0, stream, p);           \
         break;
         SDXL_LN_CASE(1) SDXL_LN_CASE(2) SDXL_LN_CASE(3) SDXL_LN_CASE(4) SDXL_LN_CASE(5) SDXL_LN_CASE(6)
         SDXL_LN_CASE(7) SDXL_LN_CASE(8) SDXL_LN_CASE(9) SDXL_LN_CASE(10) SDXL_LN_CASE(11) SDXL_LN_CASE(12)

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attention_kernels.hpp"  // kStreamOutBytes
+
 namespace sdxl_hip {
 
 // c[m, n] = w_scale[n] * sum_k a[m, k] * w[n, k] + bias[n] + residual[m, n]
