@@ -30,6 +30,7 @@ METRIC = "attention TFLOP/s + µs/call, SDXL 4096-tok self-attn b2 h10 d64 fp16"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_attention_c3_traffic.txt")
 
 
@@ -41,7 +42,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,cross,vae) and exit")
     ap.add_argument("--ceiling", action="store_true",
                     help="profiling aid: power-limited ceilings (hipBLASLt fp16 GEMM and the c3 attention on "
                          "random vs zero operands) and exit")
@@ -179,6 +180,25 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
     t = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws,
                                                 fp8_activations=True), steps, warmup)
     out["fp8_activations"]["fused_call_us"] = round(t * 1e3, 2)
+    return out
+
+
+def bench_vae_attention(torch, sh, steps=5, warmup=2):
+    """The VAE decoder mid-block's single-head FP32 attention (head_dim 512; src/cuda/vae.cpp:89-92) at
+    the latents of 1024x1024 (128x128 = 16384 tokens) and 512x512 (4096 tokens) images: device time
+    per call from captured-graph replays, seeded N(0,1) fp32 inputs."""
+    out = {}
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(512)
+    for tokens in (16384, 4096):
+        q, k, v = (torch.randn(1, tokens, 512, device="cuda:0", generator=g) for _ in range(3))
+        o = torch.empty_like(q)
+        ms = time_fn(torch, lambda: sh.attention(q, k, v, 1, out=o), steps, warmup)
+        fl = 4.0 * tokens * tokens * 512
+        out[f"tokens_{tokens}"] = {"shape": [1, 1, tokens, tokens, 512], "dtype": "fp32", "us": round(ms * 1e3, 1),
+                                   "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                                   "fp32_mfma_frac": round(fl / (ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4)}
+        del q, k, v, o
     return out
 
 
@@ -333,6 +353,9 @@ def main():
     if args.only == "cross":
         print(json.dumps(bench_cross_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
+    if args.only == "vae":
+        print(json.dumps(bench_vae_attention(torch, sh, args.steps, args.warmup)), flush=True)
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)
@@ -393,6 +416,7 @@ def main():
             del qq, kk, vv
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
         sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
+        sec["vae_mid_attention_fp32"] = bench_vae_attention(torch, sh)
         result["secondary"] = sec
 
     if not args.no_cpu:

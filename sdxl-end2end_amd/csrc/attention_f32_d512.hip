@@ -1,0 +1,268 @@
+// FP32 attention at head dimension 512 on the fp32 matrix cores.
+//
+// The SDXL VAE decoder's mid-block attention is single-head with the head
+// width equal to the 512 channels, in FP32 (reference src/cuda/vae.cpp:65-99,
+// dispatched to generic_online_attention_f32_kernel,
+// src/cuda/ops_kernels.cu:1355-1419: one block per query, keys one by one).
+// At a 128x128 latent that is 16384 tokens: 550 GFLOP per call, which the
+// per-row online kernels run at ~3 TFLOP/s. This kernel is a tiled online
+// softmax on v_mfma_f32_32x32x2_f32 with the same semantics (exact fp32
+// products, fp32 accumulation, softmax with a running maximum, output divided
+// by max(sum, 1e-20)); non-causal, unmasked calls with 16-byte aligned rows.
+//
+// Work split: a workgroup = 8 waves = 64 queries of one (batch, head): wave
+// w = 4 qt + dq owns query tile qt (32 rows) and head-dimension quarter dq
+// (128 dims) of the output, O^T[d][q] in 4 MFMA tiles (64 VGPRs). Per block
+// of 32 keys:
+//   * the 32 x 512 fp32 K tile (64 KiB) moves HBM -> LDS by DMA, double
+//     buffered (128 KiB), chunks XOR-swizzled by row so that the 32 rows'
+//     16-byte reads at one column hit distinct banks;
+//   * each wave forms the partial scores S^T = K[:, dq] Q[:, dq]^T over its
+//     128 dims (64 MFMAs), the four partials of a query tile are summed in a
+//     fixed order through LDS (16 KiB per tile, 32 KiB), so every wave of the
+//     tile holds the same full scores;
+//   * online softmax per query (the C layout gives each lane one query with
+//     16 of the 32 keys; the other 16 sit in lane l ^ 32);
+//   * O^T[d][q] += V^T P^T for the wave's 128 dims (64 MFMAs): V rows come
+//     straight from global memory (lane l reads 4 consecutive dims of one key
+//     row: the 4 accumulator tiles hold dims 128 dq + 4 m + t, t = 0..3), and
+//     P^T from the score registers, MFMA j pairing the keys held in register
+//     j by the two lane halves (the reduction order over keys is free).
+// The reduction order over the head dimension in S is likewise permuted
+// (MFMA j of group g pairs dims 8g + j and 8g + 4 + j), so every lane loads
+// its K and Q operands as 16-byte chunks.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "attention_kernels.hpp"
+
+namespace sdxl_hip {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) float lds_float;
+
+constexpr int kDim = 512;
+constexpr int kKeys = 32;                        // keys per block
+constexpr int kQuarters = 4;                     // 128-dim quarters of the head dimension
+constexpr int kRowBytes = kDim * 4;              // 2 KiB per K row
+constexpr int kTileBytes = kKeys * kRowBytes;    // 64 KiB per K tile
+constexpr int kPartFloats = 16 * 64;             // one wave's partial scores
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)(const lds_char*)p; }
+
+// One 1-KiB HBM -> LDS transfer: lane l copies 16 bytes from base + voff to
+// LDS byte lds + 16 l (base and lds wave-uniform, M0 holds the destination).
+// Inline assembly keeps the compiler from ordering it against LDS reads or
+// waiting on it; the kernel orders it explicitly (vmcnt(0) and a barrier
+// before a tile is read, the transfer into a buffer only after the barrier
+// that ends the buffer's previous reads).
+__device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint32_t lds) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint64_t ub = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    base = (const char*)(uintptr_t)ub;
+    lds = __builtin_amdgcn_readfirstlane(lds);
+    asm volatile(
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 4\n\t"
+        "global_load_lds_dwordx4 %0, %1"
+        :
+        : "v"(voff), "s"(base), "s"(lds));
+}
+
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
+
+__device__ __forceinline__ float xhalf_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
+__device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 32, 64); }
+
+// Physical 16-byte chunk of logical chunk c (0..127) in K row r: the low four
+// bits are XORed with r & 15, so 16 rows read at one logical chunk land in 16
+// distinct 16-byte bank groups.
+__device__ __forceinline__ int kchunk(int c, int r) { return c ^ (r & 15); }
+
+// kQTiles = 32-query tiles per workgroup (2: 8 waves; 1: 4 waves, for calls
+// with fewer 64-query blocks than CUs).
+template <int kQTiles>
+__global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d512_kernel(OnlineAttentionParams p, int q_blocks) {
+    constexpr int kWaves = kQTiles * kQuarters;
+    constexpr int kPerWave = 64 / kWaves;  // 1-KiB K transfers per wave and tile
+    __shared__ __attribute__((aligned(16))) char kbuf[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) float part[kWaves][kPartFloats];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int qt = wave >> 2, dq = wave & 3;
+    const int hf = lane >> 5, col = lane & 31;
+
+    const int bh = blockIdx.x / q_blocks;
+    const int q0 = (blockIdx.x % q_blocks) * (32 * kQTiles) + 32 * qt;
+    const int h = bh % p.heads, b = bh / p.heads;
+    const float* qbase = (const float*)p.q + ((int64_t)b * p.q_seq * p.q_row_stride + (int64_t)h * kDim);
+    const char* kbase = (const char*)((const float*)p.k + ((int64_t)b * p.k_seq * p.k_row_stride + (int64_t)h * kDim));
+    const float* vbase = (const float*)p.v + ((int64_t)b * p.k_seq * p.v_row_stride + (int64_t)h * kDim);
+    float* obase = (float*)p.o + ((int64_t)b * p.q_seq * p.o_row_stride + (int64_t)h * kDim);
+    const int n_blocks = (p.k_seq + kKeys - 1) / kKeys;
+    const uint32_t k_stride_b = (uint32_t)(p.k_row_stride * 4);
+
+    // K tile of key block t into buffer buf: 64 transfers of 1 KiB, kPerWave
+    // per wave; transfer n fills physical chunks 64 (n & 1) .. +63 of row n >> 1.
+    // Rows past k_seq re-read the last key (their scores are masked).
+    auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
+        const char* src = kbase + (int64_t)t * kKeys * p.k_row_stride * 4;
+        const int last = p.k_seq - 1 - t * kKeys;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int n = wave * kPerWave + j;
+            const int row = n >> 1;
+            const int c = kchunk(64 * (n & 1) + lane, row);
+            const uint32_t off = (uint32_t)min(row, last) * k_stride_b + (uint32_t)(c << 4);
+            lds_dma16(src, off, lds_addr(&kbuf[buf][0] + 1024 * n));
+        }
+    };
+    issue_k(0, 0);
+
+    // Q^T operand: lane holds query q0 + col, dims 128 dq + 8g + 4hf .. +3 in
+    // qop[g] (MFMA j of group g takes element j).
+    f32x4 qop[16];
+    {
+        const float* qrow = qbase + (int64_t)min(q0 + col, p.q_seq - 1) * p.q_row_stride + 128 * dq + 4 * hf;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) qop[g] = *(const f32x4*)(qrow + 8 * g);
+    }
+
+    const float c = p.scale * 1.4426950408889634f;  // scores to log2 units
+    f32x16 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
+    float m_run = -__builtin_inff();  // running maximum (log2 units) of this lane's query
+    float l_run = 0.0f;               // this lane's half of the running sum
+    const float* vcol = vbase + 128 * dq + 4 * col;
+    // K operand address: lane reads row col, logical chunk 32 dq + 2g + hf.
+    const int krow_off = col * kRowBytes;
+
+    for (int t = 0; t < n_blocks; ++t) {
+        const int buf = t & 1;
+        wait_vmem_all();  // this wave's part of K(t) landed
+        __syncthreads();  // all of K(t); every wave is done with K(t - 1) and the partial scores
+        if (t + 1 < n_blocks) issue_k(t + 1, buf ^ 1);
+
+        // V rows of this block for PV: register j holds key 8(j >> 2) + 4hf +
+        // (j & 3), dims 128 dq + 4 col .. +3. The first half is loaded now (in
+        // flight during S), the second after S (in flight during the score
+        // reduction, the softmax and the first half of PV).
+        f32x4 vop[16];
+        auto load_v = [&](int j0) __attribute__((always_inline)) {
+            const int key0 = t * kKeys;
+#pragma unroll
+            for (int j = j0; j < j0 + 8; ++j) {
+                const int key = min(key0 + 8 * (j >> 2) + 4 * hf + (j & 3), p.k_seq - 1);
+                vop[j] = *(const f32x4*)(vcol + (int64_t)key * p.v_row_stride);
+            }
+        };
+        load_v(0);
+
+        // partial S^T over this wave's 128 dims
+        f32x16 s;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+        const char* kt = &kbuf[buf][0] + krow_off;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const f32x4 kop = *(const lds_f32x4*)(kt + (kchunk(32 * dq + 2 * g + hf, col) << 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kop[j], qop[g][j], s, 0, 0, 0);
+        }
+        load_v(8);
+        float* mine = &part[wave][0];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mine[i * 64 + lane] = s[i];
+        __syncthreads();
+        // full scores: the tile's four partials in dq order (the same sum in every wave of the tile)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float acc = part[4 * qt][i * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < kQuarters; ++w) acc += part[4 * qt + w][i * 64 + lane];
+            s[i] = acc;
+        }
+
+        // keys past k_seq: element i is key t*32 + 8(i >> 2) + 4hf + (i & 3)
+        const int lim = p.k_seq - t * kKeys - 4 * hf;
+        if (lim < 32) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[i] = 8 * (i >> 2) + (i & 3) < lim ? s[i] : -__builtin_inff();
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = xhalf_max(mx) * c;
+        const float m_new = fmaxf(m_run, mx);  // finite: every block holds a visible key
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first block
+        m_run = m_new;
+        float pr[16];
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], c, -m_new));
+            sum += pr[i];
+        }
+        l_run = l_run * alpha + sum;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[tt][i] *= alpha;
+
+        // O^T[d][q] += V^T P^T: tile tt holds dims 128 dq + 4m + tt
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vop[j][tt], pr[j], o[tt], 0, 0, 0);
+    }
+
+    // ---- normalise and store: lane holds rows m = 8(i >> 2) + 4hf + (i & 3)
+    // of each tile for query q0 + col, i.e. dims 128 dq + 4m .. +3.
+    const float inv = 1.0f / fmaxf(xhalf_sum(l_run), 1.0e-20f);
+    if (q0 + col < p.q_seq) {
+        float* orow = obase + (int64_t)(q0 + col) * p.o_row_stride + 128 * dq;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int m = 8 * (i >> 2) + 4 * hf + (i & 3);
+            *(f32x4*)(orow + 4 * m) = f32x4{o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv};
+        }
+    }
+}
+
+}  // namespace
+
+bool attention_f32_d512_eligible(const OnlineAttentionParams& p, int dtype) {
+    auto a16 = [](const void* x) { return ((uintptr_t)x & 15) == 0; };
+    return dtype == 2 && p.head_dim == kDim && !p.causal && p.key_mask == nullptr && p.k_seq > 0 &&
+           p.q_row_stride % 4 == 0 && p.k_row_stride % 4 == 0 && p.v_row_stride % 4 == 0 && p.o_row_stride % 4 == 0 &&
+           a16(p.q) && a16(p.k) && a16(p.v) && a16(p.o) &&
+           (int64_t)kKeys * p.k_row_stride * 4 < (int64_t{1} << 31);
+}
+
+hipError_t launch_attention_f32_d512(const OnlineAttentionParams& p, int compute_units, hipStream_t stream) {
+    if (p.batch == 0 || p.q_seq == 0) return hipSuccess;
+    // 64-query workgroups (8 waves, two per SIMD) when they fill the CUs;
+    // else 32-query workgroups (4 waves): twice the workgroups, each K tile
+    // staged for half as many queries.
+    const int64_t heads_total = (int64_t)p.heads * p.batch;
+    const int64_t blocks64 = (p.q_seq + 63) / 64 * heads_total;
+    const bool wide = blocks64 >= (compute_units > 0 ? compute_units : 256);
+    const int rows = wide ? 64 : 32;
+    const int64_t q_blocks = (p.q_seq + rows - 1) / rows;
+    const int64_t grid = q_blocks * heads_total;
+    if (grid > INT32_MAX) return hipErrorInvalidValue;
+    if (wide) hipLaunchKernelGGL((attention_f32_d512_kernel<2>), dim3((unsigned)grid), dim3(512), 0, stream, p, (int)q_blocks);
+    else hipLaunchKernelGGL((attention_f32_d512_kernel<1>), dim3((unsigned)grid), dim3(256), 0, stream, p, (int)q_blocks);
+    return hipGetLastError();
+}
+
+}  // namespace sdxl_hip

@@ -70,4 +70,9 @@ struct OnlineAttentionParams {
 // dtype: 0 f16, 1 bf16, 2 f32 (sdxl_dtype values).
 hipError_t launch_online_attention(const OnlineAttentionParams& params, int dtype, hipStream_t stream);
 
+// FP32 head_dim 512 on the fp32 matrix cores (the VAE mid-block attention):
+// non-causal, unmasked, 16-byte aligned rows. Same parameters as the online kernel.
+bool attention_f32_d512_eligible(const OnlineAttentionParams& params, int dtype);
+hipError_t launch_attention_f32_d512(const OnlineAttentionParams& params, int compute_units, hipStream_t stream);
+
 }  // namespace sdxl_hip

@@ -209,7 +209,10 @@ sdxl_status sdxl_attn_fwd(const sdxl_attn_desc* d, const void* q, const void* k,
         p.batch = (int32_t)d->batch; p.q_seq = (int32_t)d->q_seq; p.k_seq = (int32_t)d->k_seq;
         p.heads = (int32_t)d->heads; p.head_dim = (int32_t)d->head_dim; p.causal = d->causal != 0;
         p.scale = scale;
-        err = sdxl_hip::launch_online_attention(p, d->dtype, s);
+        // FP32 at head_dim 512 (the VAE's attention) runs on the fp32 matrix
+        // cores when the call allows (no mask, non-causal, aligned rows).
+        if (sdxl_hip::attention_f32_d512_eligible(p, d->dtype)) err = sdxl_hip::launch_attention_f32_d512(p, compute_units(), s);
+        else err = sdxl_hip::launch_online_attention(p, d->dtype, s);
     } else {
         sdxl_hip::FusedAttentionParams p{};
         p.q = q; p.k = k; p.v = v; p.key_mask = key_mask; p.o = o;

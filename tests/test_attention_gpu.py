@@ -238,6 +238,59 @@ def test_fp32_vae_head_dim_512():
     np.testing.assert_allclose(got, oracle.attention_f32(qf, kf, vf, 1), atol=1e-5, rtol=1e-4)
 
 
+# ---------------------------------------------------------------- FP32, head_dim 512 (VAE)
+# The VAE mid-block's single-head FP32 attention (src/cuda/vae.cpp:89-92) runs on the fp32
+# matrix cores when unmasked and non-causal: 64-query workgroups, 32-key blocks, ragged tails.
+
+@pytest.mark.parametrize("B,Sq,Sk,H", [
+    (1, 1, 1, 1), (1, 33, 1, 1), (1, 64, 64, 1), (1, 100, 77, 1), (2, 257, 300, 1),
+    (1, 130, 95, 2), (1, 1024, 1024, 1)])
+def test_fp32_d512_matrix_core_kernel(B, Sq, Sk, H):
+    W = H * 512
+    qf = oracle.normal_f32(760, (B, Sq, W), 2.0)
+    kf, vf = (oracle.normal_f32(761 + i, (B, Sk, W)) for i in range(2))
+    print(f"f32 d512 B{B} Sq{Sq} Sk{Sk} H{H}", flush=True)
+    got = from_dev(sh.attention(*(torch.from_numpy(x).to(DEV) for x in (qf, kf, vf)), H))
+    ref = oracle.attention_f32(qf, kf, vf, H, threads=THREADS)
+    np.testing.assert_allclose(got, ref, atol=1e-5, rtol=1e-4)
+
+
+def test_fp32_d512_strided_rows():
+    """q, k, v as column slices of one [1, S, 3 x 512] projection (row stride 1536)."""
+    S = 200
+    qkv = oracle.normal_f32(770, (1, S, 1536))
+    d = torch.from_numpy(qkv).to(DEV)
+    got = from_dev(sh.attention(d[:, :, :512], d[:, :, 512:1024], d[:, :, 1024:], 1))
+    ref = oracle.attention_f32(*(np.ascontiguousarray(qkv[:, :, 512 * i:512 * (i + 1)]) for i in range(3)), 1)
+    np.testing.assert_allclose(got, ref, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("B,H", [(1, 1), (2, 2)])
+def test_fp32_d512_vae_latent_64x64(B, H):
+    """4096 tokens (a 512x512 image's VAE mid-block) against a float64 torch reference on the
+    device; (1, 1) runs 32-query workgroups, (2, 2) fills the CUs with 64-query workgroups."""
+    g = torch.Generator(device=DEV)
+    g.manual_seed(775)
+    q, k, v = (torch.randn(B, 4096, H * 512, device=DEV, generator=g) for _ in range(3))
+    got = sh.attention(q, k, v, H)
+    split = lambda x: x.double().view(B, 4096, H, 512).transpose(1, 2)
+    ref = torch.softmax((split(q) @ split(k).transpose(-1, -2)) / 512 ** 0.5, -1) @ split(v)
+    ref = ref.transpose(1, 2).reshape(B, 4096, H * 512)
+    err = (got.double() - ref).abs()
+    assert err.max().item() < 2e-5 and err.mean().item() < 2e-6, (err.max().item(), err.mean().item())
+
+
+def test_fp32_d512_masked_and_causal_use_the_online_kernel():
+    B, S, H = 1, 90, 1
+    qf, kf, vf = (oracle.normal_f32(780 + i, (B, S, 512)) for i in range(3))
+    mask = (np.random.default_rng(7).random((B, S)) > 0.4).astype(np.int32)
+    dev = [torch.from_numpy(x).to(DEV) for x in (qf, kf, vf)]
+    got = from_dev(sh.attention(*dev, H, key_mask=torch.from_numpy(mask).to(DEV)))
+    np.testing.assert_allclose(got, oracle.attention_f32(qf, kf, vf, H, key_mask=mask), atol=1e-5, rtol=1e-4)
+    got = from_dev(sh.attention(*dev, H, causal=True))
+    np.testing.assert_allclose(got, oracle.attention_f32(qf, kf, vf, H, causal=True), atol=1e-5, rtol=1e-4)
+
+
 @pytest.mark.parametrize("head_dim", [16, 80, 128, 160])
 def test_other_head_dims_fall_back(head_dim):
     H = 2
