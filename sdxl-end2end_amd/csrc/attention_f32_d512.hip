@@ -47,7 +47,6 @@ typedef __attribute__((address_space(3))) float lds_float;
 
 constexpr int kDim = 512;
 constexpr int kKeys = 32;                        // keys per block
-constexpr int kQuarters = 4;                     // 128-dim quarters of the head dimension
 constexpr int kRowBytes = kDim * 4;              // 2 KiB per K row
 constexpr int kTileBytes = kKeys * kRowBytes;    // 64 KiB per K tile
 constexpr int kPartFloats = 16 * 64;             // one wave's partial scores
@@ -84,18 +83,29 @@ __device__ __forceinline__ float xhalf_sum(float x) { return x + __shfl_xor(x, 3
 // distinct 16-byte bank groups.
 __device__ __forceinline__ int kchunk(int c, int r) { return c ^ (r & 15); }
 
-// kQTiles = 32-query tiles per workgroup (2: 8 waves; 1: 4 waves, for calls
-// with fewer 64-query blocks than CUs).
-template <int kQTiles>
-__global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d512_kernel(OnlineAttentionParams p, int q_blocks) {
-    constexpr int kWaves = kQTiles * kQuarters;
+template <int N> struct FloatVec;
+template <> struct FloatVec<2> { typedef float type __attribute__((ext_vector_type(2))); };
+template <> struct FloatVec<4> { typedef float type __attribute__((ext_vector_type(4))); };
+
+// kQTiles = 32-query tiles per workgroup, kSlices = slices of the head
+// dimension (512 / kSlices dims per wave): (2, 4) = 8 waves for calls with at
+// least as many 64-query blocks as CUs, else (1, 4) = 4 waves (measured at
+// 4096 tokens: 0.71 ms; (1, 8), two waves per SIMD on one query tile, 0.85).
+template <int kQTiles, int kSlices>
+__global__ __launch_bounds__(kQTiles * kSlices * 64, 1) void attention_f32_d512_kernel(OnlineAttentionParams p, int q_blocks) {
+    constexpr int kWaves = kQTiles * kSlices;
     constexpr int kPerWave = 64 / kWaves;  // 1-KiB K transfers per wave and tile
+    constexpr int kSD = kDim / kSlices;    // dims per wave
+    constexpr int kTD = kSD / 32;          // accumulator tiles per wave (dims kSD dq + kTD m + t)
+    constexpr int kG = kSD / 8;            // 4-MFMA groups of the partial scores
+    typedef typename FloatVec<kTD>::type vtype;
+    static_assert(kWaves * kPartFloats * 4 + 2 * kTileBytes <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(16))) char kbuf[2][kTileBytes];
     __shared__ __attribute__((aligned(16))) float part[kWaves][kPartFloats];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int qt = wave >> 2, dq = wave & 3;
+    const int qt = wave / kSlices, dq = wave % kSlices;
     const int hf = lane >> 5, col = lane & 31;
 
     const int bh = blockIdx.x / q_blocks;
@@ -125,25 +135,25 @@ __global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d51
     };
     issue_k(0, 0);
 
-    // Q^T operand: lane holds query q0 + col, dims 128 dq + 8g + 4hf .. +3 in
+    // Q^T operand: lane holds query q0 + col, dims kSD dq + 8g + 4hf .. +3 in
     // qop[g] (MFMA j of group g takes element j).
-    f32x4 qop[16];
+    f32x4 qop[kG];
     {
-        const float* qrow = qbase + (int64_t)min(q0 + col, p.q_seq - 1) * p.q_row_stride + 128 * dq + 4 * hf;
+        const float* qrow = qbase + (int64_t)min(q0 + col, p.q_seq - 1) * p.q_row_stride + kSD * dq + 4 * hf;
 #pragma unroll
-        for (int g = 0; g < 16; ++g) qop[g] = *(const f32x4*)(qrow + 8 * g);
+        for (int g = 0; g < kG; ++g) qop[g] = *(const f32x4*)(qrow + 8 * g);
     }
 
     const float c = p.scale * 1.4426950408889634f;  // scores to log2 units
-    f32x16 o[4];
+    f32x16 o[kTD];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < kTD; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[t][i] = 0.0f;
     float m_run = -__builtin_inff();  // running maximum (log2 units) of this lane's query
     float l_run = 0.0f;               // this lane's half of the running sum
-    const float* vcol = vbase + 128 * dq + 4 * col;
-    // K operand address: lane reads row col, logical chunk 32 dq + 2g + hf.
+    const float* vcol = vbase + kSD * dq + kTD * col;
+    // K operand address: lane reads row col, logical chunk (kSD / 4) dq + 2g + hf.
     const int krow_off = col * kRowBytes;
 
     for (int t = 0; t < n_blocks; ++t) {
@@ -153,28 +163,28 @@ __global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d51
         if (t + 1 < n_blocks) issue_k(t + 1, buf ^ 1);
 
         // V rows of this block for PV: register j holds key 8(j >> 2) + 4hf +
-        // (j & 3), dims 128 dq + 4 col .. +3. The first half is loaded now (in
+        // (j & 3), dims kSD dq + kTD col .. +kTD-1. The first half is loaded now (in
         // flight during S), the second after S (in flight during the score
         // reduction, the softmax and the first half of PV).
-        f32x4 vop[16];
+        vtype vop[16];
         auto load_v = [&](int j0) __attribute__((always_inline)) {
             const int key0 = t * kKeys;
 #pragma unroll
             for (int j = j0; j < j0 + 8; ++j) {
                 const int key = min(key0 + 8 * (j >> 2) + 4 * hf + (j & 3), p.k_seq - 1);
-                vop[j] = *(const f32x4*)(vcol + (int64_t)key * p.v_row_stride);
+                vop[j] = *(const vtype*)(vcol + (int64_t)key * p.v_row_stride);
             }
         };
         load_v(0);
 
-        // partial S^T over this wave's 128 dims
+        // partial S^T over this wave's kSD dims
         f32x16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.0f;
         const char* kt = &kbuf[buf][0] + krow_off;
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-            const f32x4 kop = *(const lds_f32x4*)(kt + (kchunk(32 * dq + 2 * g + hf, col) << 4));
+        for (int g = 0; g < kG; ++g) {
+            const f32x4 kop = *(const lds_f32x4*)(kt + (kchunk((kSD / 4) * dq + 2 * g + hf, col) << 4));
 #pragma unroll
             for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kop[j], qop[g][j], s, 0, 0, 0);
         }
@@ -183,12 +193,12 @@ __global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d51
 #pragma unroll
         for (int i = 0; i < 16; ++i) mine[i * 64 + lane] = s[i];
         __syncthreads();
-        // full scores: the tile's four partials in dq order (the same sum in every wave of the tile)
+        // full scores: the tile's partials in dq order (the same sum in every wave of the tile)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            float acc = part[4 * qt][i * 64 + lane];
+            float acc = part[kSlices * qt][i * 64 + lane];
 #pragma unroll
-            for (int w = 1; w < kQuarters; ++w) acc += part[4 * qt + w][i * 64 + lane];
+            for (int w = 1; w < kSlices; ++w) acc += part[kSlices * qt + w][i * 64 + lane];
             s[i] = acc;
         }
 
@@ -214,26 +224,29 @@ __global__ __launch_bounds__(kQTiles * kQuarters * 64, 1) void attention_f32_d51
         }
         l_run = l_run * alpha + sum;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int tt = 0; tt < kTD; ++tt)
 #pragma unroll
             for (int i = 0; i < 16; ++i) o[tt][i] *= alpha;
 
-        // O^T[d][q] += V^T P^T: tile tt holds dims 128 dq + 4m + tt
+        // O^T[d][q] += V^T P^T: tile tt holds dims kSD dq + kTD m + tt
 #pragma unroll
         for (int j = 0; j < 16; ++j)
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vop[j][tt], pr[j], o[tt], 0, 0, 0);
+            for (int tt = 0; tt < kTD; ++tt) o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vop[j][tt], pr[j], o[tt], 0, 0, 0);
     }
 
     // ---- normalise and store: lane holds rows m = 8(i >> 2) + 4hf + (i & 3)
-    // of each tile for query q0 + col, i.e. dims 128 dq + 4m .. +3.
+    // of each tile for query q0 + col, i.e. dims kSD dq + kTD m .. +kTD-1.
     const float inv = 1.0f / fmaxf(xhalf_sum(l_run), 1.0e-20f);
     if (q0 + col < p.q_seq) {
-        float* orow = obase + (int64_t)(q0 + col) * p.o_row_stride + 128 * dq;
+        float* orow = obase + (int64_t)(q0 + col) * p.o_row_stride + kSD * dq;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int m = 8 * (i >> 2) + 4 * hf + (i & 3);
-            *(f32x4*)(orow + 4 * m) = f32x4{o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv};
+            vtype w;
+#pragma unroll
+            for (int tt = 0; tt < kTD; ++tt) w[tt] = o[tt][i] * inv;
+            *(vtype*)(orow + kTD * m) = w;
         }
     }
 }
@@ -250,9 +263,9 @@ bool attention_f32_d512_eligible(const OnlineAttentionParams& p, int dtype) {
 
 hipError_t launch_attention_f32_d512(const OnlineAttentionParams& p, int compute_units, hipStream_t stream) {
     if (p.batch == 0 || p.q_seq == 0) return hipSuccess;
-    // 64-query workgroups (8 waves, two per SIMD) when they fill the CUs;
-    // else 32-query workgroups (4 waves): twice the workgroups, each K tile
-    // staged for half as many queries.
+    // 64-query workgroups (waves: 2 query tiles x 4 dim slices) when they
+    // fill the CUs; else 32-query workgroups (1 x 4): twice the workgroups,
+    // each K tile staged for half as many queries.
     const int64_t heads_total = (int64_t)p.heads * p.batch;
     const int64_t blocks64 = (p.q_seq + 63) / 64 * heads_total;
     const bool wide = blocks64 >= (compute_units > 0 ? compute_units : 256);
@@ -260,8 +273,8 @@ hipError_t launch_attention_f32_d512(const OnlineAttentionParams& p, int compute
     const int64_t q_blocks = (p.q_seq + rows - 1) / rows;
     const int64_t grid = q_blocks * heads_total;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
-    if (wide) hipLaunchKernelGGL((attention_f32_d512_kernel<2>), dim3((unsigned)grid), dim3(512), 0, stream, p, (int)q_blocks);
-    else hipLaunchKernelGGL((attention_f32_d512_kernel<1>), dim3((unsigned)grid), dim3(256), 0, stream, p, (int)q_blocks);
+    if (wide) hipLaunchKernelGGL((attention_f32_d512_kernel<2, 4>), dim3((unsigned)grid), dim3(512), 0, stream, p, (int)q_blocks);
+    else hipLaunchKernelGGL((attention_f32_d512_kernel<1, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p, (int)q_blocks);
     return hipGetLastError();
 }
 
