@@ -7,6 +7,7 @@
 // Exit status 0 on success; the first failure throws and exits 1.
 #include "sdxl_hip/ops.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -245,6 +246,31 @@ void device_cases() {
                                    Tensor::from_host_f32(runtime, vv, ScalarType::Float32), 1, false)
                          .to_host_f32(runtime);
     for (float x : vae.values) require_close(x, 3.0F, 1.0e-3F, "VAE FP32 attention");
+    // random FP32 D = 512 (the fp32 matrix-core kernel) against a float64 host softmax
+    const std::size_t vs = 70;
+    const auto vq = filled({1, vs, 512}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.37F); });
+    const auto vk = filled({1, vs, 512}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.11F); });
+    const auto vvv = filled({1, vs, 512}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.05F + 1.0F); });
+    const auto vae_rand = ops.attention(Tensor::from_host_f32(runtime, vq, ScalarType::Float32),
+                                        Tensor::from_host_f32(runtime, vk, ScalarType::Float32),
+                                        Tensor::from_host_f32(runtime, vvv, ScalarType::Float32), 1, false)
+                              .to_host_f32(runtime);
+    for (std::size_t r = 0; r < vs; ++r) {
+        std::vector<double> sc(vs);
+        double mx = -1e300, den = 0.0;
+        for (std::size_t c = 0; c < vs; ++c) {
+            double dot = 0.0;
+            for (std::size_t d = 0; d < 512; ++d) dot += (double)vq.values[r * 512 + d] * vk.values[c * 512 + d];
+            sc[c] = dot / std::sqrt(512.0);
+            mx = std::max(mx, sc[c]);
+        }
+        for (auto& x : sc) den += (x = std::exp(x - mx));
+        for (std::size_t d = 0; d < 512; ++d) {
+            double o = 0.0;
+            for (std::size_t c = 0; c < vs; ++c) o += sc[c] * vvv.values[c * 512 + d];
+            require_close(vae_rand.values[r * 512 + d], static_cast<float>(o / den), 1.0e-5F, "VAE FP32 random");
+        }
+    }
 
     // causal + key mask through the fused backend: row 0 sees only key 0.
     const auto kq = filled({1, 5, 64}, [](std::size_t i) { return std::sin(static_cast<float>(i)); });
