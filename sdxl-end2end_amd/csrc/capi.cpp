@@ -210,8 +210,10 @@ sdxl_status sdxl_attn_fwd(const sdxl_attn_desc* d, const void* q, const void* k,
         p.heads = (int32_t)d->heads; p.head_dim = (int32_t)d->head_dim; p.causal = d->causal != 0;
         p.scale = scale;
         // FP32 at head_dim 512 (the VAE's attention) runs on the fp32 matrix
-        // cores when the call allows (no mask, non-causal, aligned rows).
-        if (sdxl_hip::attention_f32_d512_eligible(p, d->dtype)) err = sdxl_hip::launch_attention_f32_d512(p, compute_units(), s);
+        // cores when the call allows (auto backend, no mask, non-causal,
+        // aligned rows); an explicit warp-online request keeps the per-row kernel.
+        if (d->backend == SDXL_ATTN_AUTO && sdxl_hip::attention_f32_d512_eligible(p, d->dtype))
+            err = sdxl_hip::launch_attention_f32_d512(p, compute_units(), s);
         else err = sdxl_hip::launch_online_attention(p, d->dtype, s);
     } else {
         sdxl_hip::FusedAttentionParams p{};

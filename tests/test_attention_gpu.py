@@ -280,6 +280,16 @@ def test_fp32_d512_vae_latent_64x64(B, H):
     assert err.max().item() < 2e-5 and err.mean().item() < 2e-6, (err.max().item(), err.mean().item())
 
 
+def test_fp32_d512_explicit_warp_online_backend():
+    """An explicit warp-online request keeps the per-row kernel; both agree with the oracle."""
+    qf, kf, vf = (oracle.normal_f32(790 + i, (1, 80, 512)) for i in range(3))
+    dev = [torch.from_numpy(x).to(DEV) for x in (qf, kf, vf)]
+    ref = oracle.attention_f32(qf, kf, vf, 1)
+    for backend in (sh.AUTO, sh.WARP_ONLINE):
+        got = from_dev(sh.attention(*dev, 1, backend=backend))
+        np.testing.assert_allclose(got, ref, atol=1e-5, rtol=1e-4)
+
+
 def test_fp32_d512_masked_and_causal_use_the_online_kernel():
     B, S, H = 1, 90, 1
     qf, kf, vf = (oracle.normal_f32(780 + i, (B, S, 512)) for i in range(3))
