@@ -145,9 +145,11 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int hf = lane >> 5, col = lane & 31;
 
-    // Tasks in row-major (m block, n block) order, each XCD taking one
-    // contiguous range: the workgroups sharing an A block run together and
-    // read it from their XCD's L2.
+    // Tasks in groups of group_m m blocks (within a group m varies fastest,
+    // then n), each XCD taking one contiguous range of tasks: an XCD's
+    // resident workgroups cover a group_m x (range / group_m) rectangle of
+    // output tiles, whose A rows and W rows together fit its L2 better than
+    // a row of the output.
     int task;
     {
         const int n = p.m_blocks * p.n_blocks;
@@ -156,7 +158,15 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
         const int per = n >> 3, extra = n & 7;
         task = xcd * per + (xcd < extra ? xcd : extra) + slot;
     }
-    const int mb = task / p.n_blocks, nb = task % p.n_blocks;
+    int mb, nb;
+    {
+        const int in_group = p.group_m * p.n_blocks;
+        const int first_m = (task / in_group) * p.group_m;
+        const int rows = min(p.m_blocks - first_m, p.group_m);
+        const int r = task % in_group;
+        mb = first_m + r % rows;
+        nb = r / rows;
+    }
     const int m0 = mb * kBMt, n0 = nb * kBN;
     const int n_stages = p.k / kBK;
 
@@ -597,6 +607,13 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
     p.m_blocks = use_tall ? (p.m + 255) / 256 : use_short ? (p.m + 63) / 64 : (p.m + 127) / 128;
     const int64_t tasks = (int64_t)p.m_blocks * p.n_blocks;
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    // Task groups of 8 m blocks for M >= 4096, row-major (groups of 1) below.
+    // Measured in the sublayer chains, where A is the previous kernel's fresh
+    // output: configs[3] (M = 8192) 142.4 -> 140.6 us with groups of 8, the
+    // level-2 cross sublayer (M = 2048) 44.0 -> 46.6 us, although each of its
+    // projections alone ran 5-8 % faster (1, 4, 8, 16 and sqrt-balanced group
+    // sizes tried on the standalone projections).
+    p.group_m = p.m < 4096 ? 1 : p.m_blocks < 8 ? p.m_blocks : 8;
     const dim3 grid((unsigned)tasks), block(256);
     // non-temporal output stores for large outputs
     const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;

@@ -23,6 +23,7 @@ struct LinearParams {
     int64_t lda, ldw, ldr, ldc;
     int32_t m, n, k;
     int32_t m_blocks, n_blocks;  // filled by the launcher
+    int32_t group_m;             // filled by the launcher: m blocks per task group
 };
 // compute_units: CUs of the device (tile-size choice).
 hipError_t launch_linear(const LinearParams& params, bool w_fp8, int compute_units, hipStream_t stream);
