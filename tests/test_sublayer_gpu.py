@@ -106,7 +106,8 @@ def _linear_ref(a_bits, w32, bias_bits=None, res_bits=None):
     return ref
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 640, 640), (129, 200, 64), (7, 1920, 640), (256, 1280, 1280)])
+@pytest.mark.parametrize("M,N,K", [(300, 640, 640), (129, 200, 64), (7, 1920, 640), (256, 1280, 1280),
+                                   (4500, 640, 640)])  # 71 m blocks: grouped task order, partial last group
 def test_linear_fp16_bias_residual(M, N, K):
     ab = oracle.normal_f16(930 + M, (M, K))
     wb = oracle.normal_f16(931 + N, (N, K), 0.02)
