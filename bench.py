@@ -42,7 +42,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,cross,vae) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae) and exit")
     ap.add_argument("--ceiling", action="store_true",
                     help="profiling aid: power-limited ceilings (hipBLASLt fp16 GEMM and the c3 attention on "
                          "random vs zero operands) and exit")
@@ -114,12 +114,12 @@ def time_fn(torch, fn, steps, warmup, reps=10):
     return e0.elapsed_time(e1) / (steps * reps)
 
 
-def bench_sublayer(torch, sh, steps=50, warmup=5):
+def bench_sublayer(torch, sh, steps=50, warmup=5, B=2, S=4096, H=10):
     """hidden [2, 4096, 640] -> LayerNorm -> fused QKV with E4M3 weights [1920, 640] and
     per-channel scales (absmax/448, N(0, 0.02) init) -> 10-head attention -> fp16 out-proj [640, 640]
     + bias + residual. Per-stage device time and the fused sdxl_attn_sublayer call, both from
-    captured-graph replays (host launch cost excluded)."""
-    B, S, H = 2, 4096, 10
+    captured-graph replays (host launch cost excluded). B, S, H select another level (level 2:
+    [2, 1024, 1280], 20 heads)."""
     W, M = H * 64, B * S
     g = torch.Generator(device="cuda:0")
     g.manual_seed(7)
@@ -153,7 +153,7 @@ def bench_sublayer(torch, sh, steps=50, warmup=5):
         "qkv_e4m3_fp8_mfma": (lambda: sh.linear_e4m3(codes.view(M, W), cscale, q8, s8, out=qkv),
                               sh.linear_flops(M, 3 * W, W), 1.0 * M * W + 3 * W * W + 2.0 * M * 3 * W),
     }
-    out = {"shape": [B, S, W], "heads": H, "w_qkv": "E4M3 [1920, 640] per-channel scales",
+    out = {"shape": [B, S, W], "heads": H, "w_qkv": f"E4M3 [{3 * W}, {W}] per-channel scales",
            "timing": "device us per call, HIP graph replay", "stages": {}}
     total = 0.0
     for name, (fn, fl, by) in stages.items():
@@ -350,6 +350,9 @@ def main():
     if args.only == "c4":
         print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
+    if args.only == "l2self":
+        print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup, B=2, S=1024, H=20)), flush=True)
+        return
     if args.only == "cross":
         print(json.dumps(bench_cross_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
@@ -415,6 +418,7 @@ def main():
                          "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
             del qq, kk, vv
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
+        sec["l2_self_sublayer"] = bench_sublayer(torch, sh, B=2, S=1024, H=20)
         sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
         sec["vae_mid_attention_fp32"] = bench_vae_attention(torch, sh)
         result["secondary"] = sec
