@@ -6,6 +6,7 @@
 // stream-ordered kernel launch. No allocation and no host synchronisation.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cctype>
 #include <cmath>
 #include <cstdint>
@@ -14,6 +15,7 @@
 
 #include "../../include/sdxl_hip/attention.h"
 #include "attention_kernels.hpp"
+#include "capi_internal.hpp"
 
 namespace {
 
@@ -26,6 +28,18 @@ sdxl_status sdxl_hip_fail(sdxl_status status, const std::string& message) {
     return status;
 }
 
+int sdxl_hip_compute_units() {
+    static std::atomic<int> cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int cus = cached[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = -1;
+        cached[dev].store(cus, std::memory_order_relaxed);
+    }
+    return cus > 0 ? cus : 0;
+}
+
 namespace {
 
 sdxl_status fail(sdxl_status status, const std::string& message) { return sdxl_hip_fail(status, message); }
@@ -34,18 +48,7 @@ int64_t eff_stride(int64_t stride, int64_t width) { return stride == 0 ? width :
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// CUs of the current device, cached per device (0 if unknown).
-int compute_units() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
-        cached[dev] = cus > 0 ? cus : -1;
-    }
-    return cached[dev] > 0 ? cached[dev] : 0;
-}
+int compute_units() { return sdxl_hip_compute_units(); }
 
 // Checks everything sdxl_attn_fwd checks that does not involve pointers.
 sdxl_status validate_desc(const sdxl_attn_desc* d) {

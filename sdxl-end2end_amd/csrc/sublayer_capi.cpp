@@ -16,18 +16,7 @@ namespace {
 
 bool aligned(const void* p, uintptr_t n) { return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; }
 
-// CUs of the current device, cached per device (0 if unknown).
-int compute_units() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-    if (cached[dev] == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 0;
-        cached[dev] = cus > 0 ? cus : -1;
-    }
-    return cached[dev] > 0 ? cached[dev] : 0;
-}
+int compute_units() { return sdxl_hip_compute_units(); }
 
 sdxl_status launch_status(hipError_t err, const char* what) {
     if (err != hipSuccess)
