@@ -123,22 +123,25 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 // (64-byte rows, chunk swizzle (row >> 2) & 3) and are decoded when the
 // operand is read; fp16 weights use the A-operand layout. kAFp8 (with kWFp8):
 // E4M3 activations in 64-byte rows, fp8 MFMA.
-template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt>
-__global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
+template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2>
+__global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p) {
     static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
     constexpr int kBMt = 64 * kTM;
+    constexpr int kWaves = 2 * kWM;            // kWM waves along M x 2 along N
+    constexpr int kTMw = kBMt / (32 * kWM);    // 32-row MFMA tiles per wave
+    static_assert(kTMw >= 1 && kTMw * 32 * kWM == kBMt, "wave tiling");
     constexpr int kWRowBytes = kWFp8 ? 64 : kRowBytes;
     constexpr int kARowBytes = kAFp8 ? 64 : kRowBytes;
     constexpr int kATileBytes = kBMt * kARowBytes;
     constexpr int kWTileBytes = 128 * kWRowBytes;
-    constexpr int kAXfers = kAFp8 ? kBMt / 64 : kBMt / 32;  // 1-KiB A transfers per wave and stage
-    constexpr int kWXfers = kWFp8 ? 2 : 4;
+    constexpr int kAXfers = kATileBytes / 1024 / kWaves;  // 1-KiB A transfers per wave and stage
+    constexpr int kWXfers = kWTileBytes / 1024 / kWaves;
     constexpr int kLoadsPerStage = kAXfers + kWXfers;
     // Stage st: A tile at smem[st], W tile right after it. The epilogue
     // reuses the array.
     // (at least the epilogue's 4 x 32 x 256 bytes of staging)
     constexpr int kStageBytes = kATileBytes + kWTileBytes;
-    constexpr int kSmemStages = kRing * kStageBytes >= 4 * 32 * 256 ? kRing : (4 * 32 * 256 + kStageBytes - 1) / kStageBytes;
+    constexpr int kSmemStages = kRing * kStageBytes >= kWaves * 32 * 256 ? kRing : (kWaves * 32 * 256 + kStageBytes - 1) / kStageBytes;
     __shared__ __attribute__((aligned(16))) char smem[kSmemStages][kStageBytes];
 
     const int lane = threadIdx.x & 63;
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
 
     // Epilogue column constants, loaded now so that their latency hides under
     // the main loop: lane l finishes columns 4(l%16) .. +3 of its wave block.
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % kWM, wn = wave / kWM;
     const int ec = lane & 15;
     const int en = n0 + wn * 64 + 4 * ec;
     const bool en_ok = en < p.n;
@@ -227,17 +230,17 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
 
     // ---- wave block: rows wm*32kTM .. +32kTM, columns wn*64 .. +64;
     // acc[j][i] = C^T tile of n-tile j and m-tile i.
-    f32x16 acc[2][kTM];
+    f32x16 acc[2][kTMw];
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < kTM; ++i)
+        for (int i = 0; i < kTMw; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.0f;
-    int a_off[kTM], a_swz[kTM], w_off[2], w_swz[2];
+    int a_off[kTMw], a_swz[kTMw], w_off[2], w_swz[2];
 #pragma unroll
-    for (int t = 0; t < kTM; ++t) {
-        const int ar = wm * 32 * kTM + 32 * t + col;
+    for (int t = 0; t < kTMw; ++t) {
+        const int ar = wm * 32 * kTMw + 32 * t + col;
         a_off[t] = ar * kARowBytes;
         a_swz[t] = kAFp8 ? (ar >> 2) & 3 : swz(ar);
     }
@@ -276,13 +279,13 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 const u32x4 hi = *(const lds_u32x4*)(tile + off + (((2 * hf + 1) ^ sw) << 4));
                 return __builtin_bit_cast(i32x8, u32x4x2{lo, hi});
             };
-            i32x8 wop8[2], aop8[kTM];
+            i32x8 wop8[2], aop8[kTMw];
 #pragma unroll
             for (int t = 0; t < 2; ++t) wop8[t] = op32(wb, w_off[t] - hf * 8, w_swz[t]);
 #pragma unroll
-            for (int t = 0; t < kTM; ++t) aop8[t] = op32(ab, a_off[t], a_swz[t]);
+            for (int t = 0; t < kTMw; ++t) aop8[t] = op32(ab, a_off[t], a_swz[t]);
 #pragma unroll
-            for (int i = 0; i < kTM; ++i)
+            for (int i = 0; i < kTMw; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[j][i] = mfma32_fp8(wop8[j], aop8[i], acc[j][i]);
             continue;
@@ -291,9 +294,9 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
         // (two register sets), so the LDS latency is not exposed at one or two
         // waves per SIMD. E4M3 weights are read as codes and decoded just
         // before their step.
-        i16x8 aop[2][kTM];
+        i16x8 aop[2][kTMw];
         u32x4 wraw[2][2];  // fp16: the operand; E4M3: codes in the first two dwords
-        auto read_ops = [&](int ks, i16x8 (&a)[kTM], u32x4 (&w)[2]) __attribute__((always_inline)) {
+        auto read_ops = [&](int ks, i16x8 (&a)[kTMw], u32x4 (&w)[2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if constexpr (kWFp8) {
@@ -304,7 +307,7 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 }
             }
 #pragma unroll
-            for (int t = 0; t < kTM; ++t)
+            for (int t = 0; t < kTMw; ++t)
                 a[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
         };
         read_ops(0, aop[0], wraw[0]);
@@ -324,7 +327,7 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
                 }
             }
 #pragma unroll
-            for (int i = 0; i < kTM; ++i)
+            for (int i = 0; i < kTMw; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[j][i] = mfma32(wop[j], aop[cur][i], acc[j][i]);
             __builtin_amdgcn_sched_barrier(0);
@@ -342,11 +345,11 @@ __global__ __launch_bounds__(256, kOcc) void linear_kernel(LinearParams p) {
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
     char* eb = &smem[0][0] + wave * (32 * 256);
-    static_assert(sizeof(smem) >= 4 * 32 * 256, "epilogue staging fits in the stage buffers");
+    static_assert(sizeof(smem) >= kWaves * 32 * 256, "epilogue staging fits in the stage buffers");
     __syncthreads();  // every wave is done with the stage buffers
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-        const int rm0 = m0 + wm * 32 * kTM + 32 * i + (lane >> 4);  // row of iteration it: rm0 + 4 it
+    for (int i = 0; i < kTMw; ++i) {
+        const int rm0 = m0 + wm * 32 * kTMw + 32 * i + (lane >> 4);  // row of iteration it: rm0 + 4 it
         f16x4 res[8];
         float rs[8];  // activation scale of the row (1 for fp16 activations)
 #pragma unroll
@@ -622,6 +625,20 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
         if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, true>), grid, block, 0, stream, p);      \
         else hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, false>), grid, block, 0, stream, p);        \
     } while (0)
+    // FP8 activations: 256 x 128 tiles of 8 waves (4 x 2, each 64 x 64; two
+    // workgroups per CU) when those tiles give at least 90 % of the CUs one:
+    // twice the rows per staged W tile (measured: 8192 x 1920 x 640 19.9 ->
+    // 16.7 us, 2048 x 3840 x 1280 19.2 -> 16.3 us; fewer tiles, e.g. the
+    // out-projections, ran slower). For fp16 / E4M3-weight operands the same
+    // tiles measured within 4 % of the 4-wave grids.
+    if (a_fp8 && (int64_t)((p.m + 255) / 256) * p.n_blocks * 10 >= (int64_t)(compute_units > 0 ? compute_units : 256) * 9) {
+        p.m_blocks = (p.m + 255) / 256;
+        p.group_m = p.m < 4096 ? 1 : p.m_blocks < 8 ? p.m_blocks : 8;
+        const dim3 g8((unsigned)((int64_t)p.m_blocks * p.n_blocks)), b8(512);
+        if (nt) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, true, 4>), g8, b8, 0, stream, p);
+        else hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, false, 4>), g8, b8, 0, stream, p);
+        return hipGetLastError();
+    }
     if (a_fp8) {
         if (use_tall) SDXL_LIN(true, true, 4, 3);
         else if (use_short) SDXL_LIN(true, true, 1, 2);
