@@ -625,18 +625,25 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
         if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, true>), grid, block, 0, stream, p);      \
         else hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, false>), grid, block, 0, stream, p);        \
     } while (0)
-    // FP8 activations: 256 x 128 tiles of 8 waves (4 x 2, each 64 x 64; two
+    // E4M3 weights: 256 x 128 tiles of 8 waves (4 x 2, each 64 x 64; two
     // workgroups per CU) when those tiles give at least 90 % of the CUs one:
-    // twice the rows per staged W tile (measured: 8192 x 1920 x 640 19.9 ->
-    // 16.7 us, 2048 x 3840 x 1280 19.2 -> 16.3 us; fewer tiles, e.g. the
-    // out-projections, ran slower). For fp16 / E4M3-weight operands the same
-    // tiles measured within 4 % of the 4-wave grids.
-    if (a_fp8 && (int64_t)((p.m + 255) / 256) * p.n_blocks * 10 >= (int64_t)(compute_units > 0 ? compute_units : 256) * 9) {
+    // each staged W tile serves twice the rows, four waves share each SIMD.
+    // Measured: 8192 x 1920 x 640 with E4M3 activations 19.9 -> 16.7 us, fp16
+    // activations 30-32 -> 27.5-30 us (configs[3] sublayer stage 29.5 -> 24.9);
+    // 2048 x 3840 x 1280 19.2 -> 16.3 and 28.2 -> 26.6 us. With fewer tiles
+    // (the out-projections) they ran slower; fp16 weights (48-KiB stages, one
+    // workgroup per CU) measured within 2 %, so those keep the 4-wave grids.
+    if (w_fp8 && (int64_t)((p.m + 255) / 256) * p.n_blocks * 10 >= (int64_t)(compute_units > 0 ? compute_units : 256) * 9) {
         p.m_blocks = (p.m + 255) / 256;
         p.group_m = p.m < 4096 ? 1 : p.m_blocks < 8 ? p.m_blocks : 8;
         const dim3 g8((unsigned)((int64_t)p.m_blocks * p.n_blocks)), b8(512);
-        if (nt) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, true, 4>), g8, b8, 0, stream, p);
-        else hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, false, 4>), g8, b8, 0, stream, p);
+        if (a_fp8) {
+            if (nt) hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, true, 4>), g8, b8, 0, stream, p);
+            else hipLaunchKernelGGL((linear_kernel<true, true, 4, 3, 2, false, 4>), g8, b8, 0, stream, p);
+        } else {
+            if (nt) hipLaunchKernelGGL((linear_kernel<true, false, 4, 2, 2, true, 4>), g8, b8, 0, stream, p);
+            else hipLaunchKernelGGL((linear_kernel<true, false, 4, 2, 2, false, 4>), g8, b8, 0, stream, p);
+        }
         return hipGetLastError();
     }
     if (a_fp8) {
