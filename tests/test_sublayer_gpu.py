@@ -120,16 +120,22 @@ def test_linear_fp16_bias_residual(M, N, K):
     within_half_ulp(plain, _linear_ref(ab, oracle.f16_bits_to_f32(wb)), 1e-4, "linear fp16 plain")
 
 
-@pytest.mark.parametrize("M", [8192, 8100, 333])
-def test_linear_e4m3_qkv(M):
-    """configs[3] fused QKV projection: [M, 640] x E4M3 [1920, 640] with per-row scales."""
-    K, N = 640, 1920
+@pytest.mark.parametrize("M,N", [(8192, 1920), (8100, 1920), (333, 1920), (8192, 1000)])
+def test_linear_e4m3_qkv(M, N):
+    """configs[3] fused QKV projection: [M, 640] x E4M3 [1920, 640] with per-row scales (M >= 8100:
+    256 x 128 tiles of 8 waves; N = 1000: a ragged last column tile, with bias and residual)."""
+    K = 640
     ab = oracle.normal_f16(940, (M, K))
     Wf = oracle.normal_f32(941, (N, K), 0.02)
     q, s = oracle.quantize_e4m3_rows(Wf)
-    got = host(sh.linear(dev16(ab), torch.from_numpy(q).to(DEV), w_scale=torch.from_numpy(s).to(DEV)))
-    rows = np.r_[0:64, M // 2:M // 2 + 32, M - 64:M] if M > 512 else np.arange(M)
-    ref = _linear_ref(ab[rows], oracle.dequantize_e4m3_rows(q, s))
+    extras = N % 128 != 0
+    bb = oracle.normal_f16(942, (N,), 0.02) if extras else None
+    rb = oracle.normal_f16(943, (M, N)) if extras else None
+    got = host(sh.linear(dev16(ab), torch.from_numpy(q).to(DEV), w_scale=torch.from_numpy(s).to(DEV),
+                         bias=dev16(bb) if extras else None, residual=dev16(rb) if extras else None))
+    # the first 256-row tile whole (all four wave rows), a middle block, the last rows
+    rows = np.r_[0:256, M // 2:M // 2 + 32, M - 64:M] if M > 512 else np.arange(M)
+    ref = _linear_ref(ab[rows], oracle.dequantize_e4m3_rows(q, s), bb, rb[rows] if extras else None)
     within_half_ulp(got[rows], ref, 1e-4, f"linear E4M3 {M}x{N}x{K}")
 
 
@@ -250,7 +256,7 @@ def test_linear_e4m3_activations(M, N, K, extras):
     t = lambda x: torch.from_numpy(x).to(DEV)
     got = host(sh.linear_e4m3(t(aq), t(a_s), t(wq), t(w_s), bias=dev16(bb) if extras else None,
                               residual=dev16(rb) if extras else None))
-    rows = np.r_[0:64, M // 2:M // 2 + 32, M - 64:M] if M > 512 else np.arange(M)
+    rows = np.r_[0:256, M // 2:M // 2 + 32, M - 64:M] if M > 512 else np.arange(M)
     ref = oracle.dequantize_e4m3_rows(aq[rows], a_s[rows]).astype(np.float64) @ \
         oracle.dequantize_e4m3_rows(wq, w_s).astype(np.float64).T
     if extras:
