@@ -479,13 +479,21 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
         const float scale = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
         if (lane == 0) p.y_scale[row] = scale;
         uint16_t* q = (uint16_t*)((uint8_t*)p.y + row * p.ldy);
+        // y / scale correctly rounded, as the weight quantiser divides, from
+        // the correctly rounded reciprocal r (one division per row) and one
+        // Markstein correction per value: q = y r, e = y - q scale (exact by
+        // fma), q + e r rounds to the nearest quotient.
+        const float r = 1.0f / scale;
+        auto quot = [&](float y) __attribute__((always_inline)) {
+            const float q0 = y * r;
+            return __builtin_fmaf(__builtin_fmaf(-q0, scale, y), r, q0);
+        };
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             const int c = lane + 64 * j;
             if (c < pairs) {
-                // y / scale correctly rounded, as the weight quantiser divides
-                const float q0 = fminf(fmaxf(yv[2 * j] / scale, -448.0f), 448.0f);
-                const float q1 = fminf(fmaxf(yv[2 * j + 1] / scale, -448.0f), 448.0f);
+                const float q0 = fminf(fmaxf(quot(yv[2 * j]), -448.0f), 448.0f);
+                const float q1 = fminf(fmaxf(quot(yv[2 * j + 1]), -448.0f), 448.0f);
                 store_out<kNt>((uint16_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q0, q1, 0u, false) & 0xFFFFu), q + c);
             }
         }
