@@ -517,7 +517,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
 // and stores), otherwise as layer_norm_kernel (same two-pass centred variance,
 // fp32 maths, one rounding). kChunks = ceil(width / 512).
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-template <int kChunks, bool kNt>
+template <int kChunks, bool kNt, bool kE4M3>
 __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -555,6 +555,43 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
     const float inv = 1.0f / sqrtf(var + p.eps);
     const f16x8v* g = (const f16x8v*)p.gamma;
     const f16x8v* bt = (const f16x8v*)p.beta;
+    if constexpr (kE4M3) {
+        // as layer_norm_kernel's E4M3 form: row amax, scale, correctly rounded
+        // quotients (reciprocal + one Markstein correction), 8 codes per lane
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int c = min(lane + 64 * j, chunks - 1);
+            const f16x8v gg = g[c], bb = bt[c];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[8 * j + e] = (v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e];
+            if (lane + 64 * j < chunks)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[8 * j + e]));
+        }
+        amax = wave_max(amax);
+        const float scale = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
+        if (lane == 0) p.y_scale[row] = scale;
+        const float r = 1.0f / scale;
+        auto code4 = [&](const float* y4) __attribute__((always_inline)) {
+            float q[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float q0 = y4[e] * r;
+                q[e] = fminf(fmaxf(__builtin_fmaf(__builtin_fmaf(-q0, scale, y4[e]), r, q0), -448.0f), 448.0f);
+            }
+            const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0u, false);
+            return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+        };
+        typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+        u32x2v* yq = (u32x2v*)((uint8_t*)p.y + row * p.ldy);
+#pragma unroll
+        for (int j = 0; j < kChunks; ++j) {
+            const int c = lane + 64 * j;
+            if (c < chunks) store_out<kNt>(u32x2v{code4(v + 8 * j), code4(v + 8 * j + 4)}, yq + c);
+        }
+        return;
+    }
     f16x8v* y = (f16x8v*)((_Float16*)p.y + row * p.ldy);
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
@@ -677,17 +714,23 @@ hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t strea
     const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
     const bool e4m3 = p.y_scale != nullptr;
     const bool nt = p.rows * p.width * (e4m3 ? 1 : 2) >= kStreamOutBytes;  // non-temporal stores for large outputs
-    // 16-byte form for fp16 output: width % 8 == 0, 16-byte aligned rows
-    // (measured: [2048, 1280] 4.9 -> 4.0 us; [8192, 640] unchanged). The E4M3
-    // form stays on the pair kernel: its correctly rounded divisions run for
-    // every lane of a partly used 8-wide chunk (width 640: 9.7 vs 7.7 us).
-    const bool v8 = !e4m3 && p.width % 8 == 0 && p.ldx % 8 == 0 && p.ldy % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
-                    ((uintptr_t)p.y & 15) == 0 && ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0;
+    // 16-byte form: width % 8 == 0, 16-byte aligned input rows, 16-byte (fp16)
+    // or 8-byte (E4M3) aligned output rows. Measured: fp16 [2048, 1280] 4.9 ->
+    // 4.0 us, [8192, 640] unchanged; E4M3 [2048, 1280] 4.7 -> 4.3 us,
+    // [1024, 2048] 4.5 -> 4.1 us, but width 640 (80 chunks: a quarter of the
+    // lanes take two) 7.3 -> 7.6 us, so E4M3 rows narrower than 1024 keep the
+    // pair kernel.
+    const bool v8 = p.width % 8 == 0 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+                    ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 &&
+                    (e4m3 ? p.width >= 1024 && p.ldy % 8 == 0 && ((uintptr_t)p.y & 7) == 0
+                          : p.ldy % 8 == 0 && ((uintptr_t)p.y & 15) == 0);
     if (v8) {
         switch ((p.width + 511) / 512) {
 #define SDXL_LN8(n)                                                                                   \
-    if (nt) hipLaunchKernelGGL((layer_norm_v8_kernel<n, true>), grid, block, 0, stream, p);        \
-    else hipLaunchKernelGGL((layer_norm_v8_kernel<n, false>), grid, block, 0, stream, p);
+    if (e4m3 && nt) hipLaunchKernelGGL((layer_norm_v8_kernel<n, true, true>), grid, block, 0, stream, p);       \
+    else if (e4m3) hipLaunchKernelGGL((layer_norm_v8_kernel<n, false, true>), grid, block, 0, stream, p);      \
+    else if (nt) hipLaunchKernelGGL((layer_norm_v8_kernel<n, true, false>), grid, block, 0, stream, p);        \
+    else hipLaunchKernelGGL((layer_norm_v8_kernel<n, false, false>), grid, block, 0, stream, p);
         case 1: SDXL_LN8(1) break;
         case 2: SDXL_LN8(2) break;
         case 3: SDXL_LN8(3) break;
