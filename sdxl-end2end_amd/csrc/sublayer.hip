@@ -136,6 +136,8 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
     constexpr int kWTileBytes = 128 * kWRowBytes;
     constexpr int kAXfers = kATileBytes / 1024 / kWaves;  // 1-KiB A transfers per wave and stage
     constexpr int kWXfers = kWTileBytes / 1024 / kWaves;
+    static_assert(kAXfers * kWaves * 1024 == kATileBytes && kWXfers * kWaves * 1024 == kWTileBytes,
+                  "every 1-KiB transfer of a stage has a wave");
     constexpr int kLoadsPerStage = kAXfers + kWXfers;
     // Stage st: A tile at smem[st], W tile right after it. The epilogue
     // reuses the array.
