@@ -104,7 +104,9 @@ sdxl_status sdxl_attn_backend_parse(const char* name, int32_t* backend);
 const char* sdxl_attn_backend_name(int32_t backend);
 
 /* Name of the kernel family a resolved backend runs on this device:
- * "flash-gfx950" or "wave-online". */
+ * "flash-gfx950" or "wave-online". Under the auto backend, unmasked non-causal
+ * FP32 calls at head_dim 512 (the VAE's attention) resolve to the online
+ * family but run its fp32 matrix-core kernel. */
 const char* sdxl_attn_kernel_name(int32_t resolved_backend);
 
 const char* sdxl_status_string(sdxl_status status);
