@@ -48,7 +48,9 @@ typedef enum sdxl_dtype {
  *     two "fast" backends it replaces);
  *   WARP_ONLINE runs the wave64 online-softmax kernel (the reference's
  *     correctness fallback, any head_dim <= 1024, f16/bf16/f32);
- *   AUTO picks the fused kernel whenever it is eligible, else WARP_ONLINE. */
+ *   AUTO picks the fused kernel whenever it is eligible, else WARP_ONLINE,
+ *     whose unmasked non-causal FP32 calls at head_dim 512 (the VAE) run a
+ *     tiled fp32 matrix-core kernel instead of the per-row one. */
 typedef enum sdxl_attn_backend {
     SDXL_ATTN_AUTO = 0,
     SDXL_ATTN_CUDNN_SDPA = 1,
