@@ -251,6 +251,169 @@ __global__ __launch_bounds__(kQTiles * kSlices * 64, 1) void attention_f32_d512_
     }
 }
 
+// Variant for calls with fewer 32-query tiles than CUs (the VAE at a 64x64
+// latent, 4096 tokens: 128 tiles): 16-query workgroups on
+// v_mfma_f32_16x16x4_f32, 4 waves = 4 slices of 128 dims, so twice as many
+// workgroups fill the CUs. Same algorithm and order of operations as above
+// per key block; the 16x16 C layout gives lane l query l & 15 and keys
+// 4 (l >> 4) .. +3 of each 16-key half, so the row maximum and sum take two
+// lane exchanges (l ^ 16, l ^ 32). Index maps (free reduction orders):
+//   S: MFMA j of group g pairs dim 16 g + 4 (l >> 4) + j of the slice (K and
+//      Q operands are 16-byte chunks);
+//   PV: score register r (key 16 (r >> 2) + 4 (l >> 4) + (r & 3)) is the B
+//      operand of MFMA r; accumulator tile tt row m holds dim 8 m + tt of the
+//      slice, so lane l loads dims 8 (l & 15) .. +7 of its key row (32 bytes)
+//      and stores 8 consecutive dims per register.
+__global__ __launch_bounds__(256, 1) void attention_f32_d512_q16_kernel(OnlineAttentionParams p, int q_blocks) {
+    constexpr int kWaves = 4;
+    constexpr int kPerWave = 64 / kWaves;
+    constexpr int kSD = kDim / kWaves;  // 128 dims per wave
+    static_assert(kWaves * 8 * 64 * 4 + 2 * kTileBytes <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(16))) char kbuf[2][kTileBytes];
+    __shared__ __attribute__((aligned(16))) float part[kWaves][8 * 64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int dq = wave;
+    const int qc = lane & 15, kq = lane >> 4;
+
+    const int bh = blockIdx.x / q_blocks;
+    const int q0 = (blockIdx.x % q_blocks) * 16;
+    const int h = bh % p.heads, b = bh / p.heads;
+    const float* qbase = (const float*)p.q + ((int64_t)b * p.q_seq * p.q_row_stride + (int64_t)h * kDim);
+    const char* kbase = (const char*)((const float*)p.k + ((int64_t)b * p.k_seq * p.k_row_stride + (int64_t)h * kDim));
+    const float* vbase = (const float*)p.v + ((int64_t)b * p.k_seq * p.v_row_stride + (int64_t)h * kDim);
+    float* obase = (float*)p.o + ((int64_t)b * p.q_seq * p.o_row_stride + (int64_t)h * kDim);
+    const int n_blocks = (p.k_seq + kKeys - 1) / kKeys;
+    const uint32_t k_stride_b = (uint32_t)(p.k_row_stride * 4);
+
+    // K tile of key block t into buffer buf (as in the 32-query kernel).
+    auto issue_k = [&](int t, int buf) __attribute__((always_inline)) {
+        const char* src = kbase + (int64_t)t * kKeys * p.k_row_stride * 4;
+        const int last = p.k_seq - 1 - t * kKeys;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int n = wave * kPerWave + j;
+            const int row = n >> 1;
+            const int c = kchunk(64 * (n & 1) + lane, row);
+            const uint32_t off = (uint32_t)min(row, last) * k_stride_b + (uint32_t)(c << 4);
+            lds_dma16(src, off, lds_addr(&kbuf[buf][0] + 1024 * n));
+        }
+    };
+    issue_k(0, 0);
+
+    // Q operand: query q0 + qc, dims kSD dq + 16 g + 4 kq .. +3 in qop[g].
+    f32x4 qop[8];
+    {
+        const float* qrow = qbase + (int64_t)min(q0 + qc, p.q_seq - 1) * p.q_row_stride + kSD * dq + 4 * kq;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) qop[g] = *(const f32x4*)(qrow + 16 * g);
+    }
+
+    const float c = p.scale * 1.4426950408889634f;  // scores to log2 units
+    f32x4 o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -__builtin_inff();
+    float l_run = 0.0f;  // this lane's quarter of the running sum
+    const float* vcol = vbase + kSD * dq + 8 * qc;
+
+    for (int t = 0; t < n_blocks; ++t) {
+        const int buf = t & 1;
+        wait_vmem_all();
+        __syncthreads();
+        if (t + 1 < n_blocks) issue_k(t + 1, buf ^ 1);
+
+        // V operands: register r holds key t*32 + 16 (r >> 2) + 4 kq + (r & 3),
+        // dims kSD dq + 8 qc .. +7 (two 16-byte halves).
+        f32x4 vop[8][2];
+        auto load_v = [&](int r0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int r = r0; r < r0 + 4; ++r) {
+                const int key = min(t * kKeys + 16 * (r >> 2) + 4 * kq + (r & 3), p.k_seq - 1);
+                const float* src = vcol + (int64_t)key * p.v_row_stride;
+                vop[r][0] = *(const f32x4*)src;
+                vop[r][1] = *(const f32x4*)(src + 4);
+            }
+        };
+        load_v(0);
+
+        f32x4 s[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            s[kt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const int row = 16 * kt + qc;
+            const char* krow = &kbuf[buf][0] + row * kRowBytes;
+#pragma unroll
+            for (int g = 0; g < 8; ++g) {
+                const f32x4 kop = *(const lds_f32x4*)(krow + (kchunk((kSD / 4) * dq + 4 * g + kq, row) << 4));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kop[j], qop[g][j], s[kt], 0, 0, 0);
+            }
+        }
+        load_v(4);
+        float* mine = &part[wave][0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mine[i * 64 + lane] = s[i >> 2][i & 3];
+        __syncthreads();
+        // full scores: the partials summed in slice order
+        float sc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float acc = part[0][i * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) acc += part[w][i * 64 + lane];
+            sc[i] = acc;
+        }
+
+        // keys past k_seq: score i is key t*32 + 16 (i >> 2) + 4 kq + (i & 3)
+        const int lim = p.k_seq - t * kKeys - 4 * kq;
+        if (lim < 32) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sc[i] = 16 * (i >> 2) + (i & 3) < lim ? sc[i] : -__builtin_inff();
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, sc[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+        const float m_new = fmaxf(m_run, mx);  // finite: every block holds a visible key
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float pr[8];
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], c, -m_new));
+            sum += pr[i];
+        }
+        l_run = l_run * alpha + sum;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) o[tt] *= alpha;
+
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt)
+                o[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vop[r][tt >> 2][tt & 3], pr[r], o[tt], 0, 0, 0);
+    }
+
+    // ---- normalise and store: register i of tile tt is dim kSD dq + 8 (4 kq + i) + tt.
+    float l = l_run + __shfl_xor(l_run, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.0f / fmaxf(l, 1.0e-20f);
+    if (q0 + qc < p.q_seq) {
+        float* orow = obase + (int64_t)(q0 + qc) * p.o_row_stride + kSD * dq + 32 * kq;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 lo = {o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv};
+            const f32x4 hi = {o[4][i] * inv, o[5][i] * inv, o[6][i] * inv, o[7][i] * inv};
+            *(f32x4*)(orow + 8 * i) = lo;
+            *(f32x4*)(orow + 8 * i + 4) = hi;
+        }
+    }
+}
+
 }  // namespace
 
 bool attention_f32_d512_eligible(const OnlineAttentionParams& p, int dtype) {
@@ -265,15 +428,19 @@ hipError_t launch_attention_f32_d512(const OnlineAttentionParams& p, int compute
     if (p.batch == 0 || p.q_seq == 0) return hipSuccess;
     // 64-query workgroups (waves: 2 query tiles x 4 dim slices) when they
     // fill the CUs; else 32-query workgroups (1 x 4): twice the workgroups,
-    // each K tile staged for half as many queries.
+    // each K tile staged for half as many queries; and when even those leave
+    // CUs idle, 16-query workgroups on the 16x16 matrix-core tiles.
     const int64_t heads_total = (int64_t)p.heads * p.batch;
     const int64_t blocks64 = (p.q_seq + 63) / 64 * heads_total;
-    const bool wide = blocks64 >= (compute_units > 0 ? compute_units : 256);
-    const int rows = wide ? 64 : 32;
+    const int cus = compute_units > 0 ? compute_units : 256;
+    const bool wide = blocks64 >= cus;
+    const bool q16 = !wide && (p.q_seq + 31) / 32 * heads_total < cus;
+    const int rows = wide ? 64 : q16 ? 16 : 32;
     const int64_t q_blocks = (p.q_seq + rows - 1) / rows;
     const int64_t grid = q_blocks * heads_total;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
-    if (wide) hipLaunchKernelGGL((attention_f32_d512_kernel<2, 4>), dim3((unsigned)grid), dim3(512), 0, stream, p, (int)q_blocks);
+    if (q16) hipLaunchKernelGGL(attention_f32_d512_q16_kernel, dim3((unsigned)grid), dim3(256), 0, stream, p, (int)q_blocks);
+    else if (wide) hipLaunchKernelGGL((attention_f32_d512_kernel<2, 4>), dim3((unsigned)grid), dim3(512), 0, stream, p, (int)q_blocks);
     else hipLaunchKernelGGL((attention_f32_d512_kernel<1, 4>), dim3((unsigned)grid), dim3(256), 0, stream, p, (int)q_blocks);
     return hipGetLastError();
 }

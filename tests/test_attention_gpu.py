@@ -240,11 +240,13 @@ def test_fp32_vae_head_dim_512():
 
 # ---------------------------------------------------------------- FP32, head_dim 512 (VAE)
 # The VAE mid-block's single-head FP32 attention (src/cuda/vae.cpp:89-92) runs on the fp32
-# matrix cores when unmasked and non-causal: 64-query workgroups, 32-key blocks, ragged tails.
+# matrix cores when unmasked and non-causal: 64-, 32- or 16-query workgroups (by how many fill the
+# CUs), 32-key blocks, ragged tails. The small shapes run 16-query workgroups; Sq 8192 (one head)
+# 32-query ones, Sq 16384 64-query ones.
 
 @pytest.mark.parametrize("B,Sq,Sk,H", [
     (1, 1, 1, 1), (1, 33, 1, 1), (1, 64, 64, 1), (1, 100, 77, 1), (2, 257, 300, 1),
-    (1, 130, 95, 2), (1, 1024, 1024, 1)])
+    (1, 130, 95, 2), (1, 1024, 1024, 1), (1, 8192, 100, 1), (1, 16384, 70, 1)])
 def test_fp32_d512_matrix_core_kernel(B, Sq, Sk, H):
     W = H * 512
     qf = oracle.normal_f32(760, (B, Sq, W), 2.0)
@@ -265,10 +267,11 @@ def test_fp32_d512_strided_rows():
     np.testing.assert_allclose(got, ref, atol=1e-5, rtol=1e-4)
 
 
-@pytest.mark.parametrize("B,H", [(1, 1), (2, 2)])
+@pytest.mark.parametrize("B,H", [(1, 1), (2, 1), (2, 2)])
 def test_fp32_d512_vae_latent_64x64(B, H):
     """4096 tokens (a 512x512 image's VAE mid-block) against a float64 torch reference on the
-    device; (1, 1) runs 32-query workgroups, (2, 2) fills the CUs with 64-query workgroups."""
+    device; (1, 1) runs 16-query workgroups, (2, 1) 32-query ones, (2, 2) fills the CUs with
+    64-query workgroups."""
     g = torch.Generator(device=DEV)
     g.manual_seed(775)
     q, k, v = (torch.randn(B, 4096, H * 512, device=DEV, generator=g) for _ in range(3))
