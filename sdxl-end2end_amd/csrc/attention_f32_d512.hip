@@ -178,16 +178,24 @@ __global__ __launch_bounds__(kQTiles * kSlices * 64, 1) void attention_f32_d512_
         load_v(0);
 
         // partial S^T over this wave's kSD dims
-        f32x16 s;
+        // two accumulator chains (even and odd groups), summed after: at 16384
+        // tokens 5.12 -> 5.00 ms against one chain (the same interleave in the
+        // 16-query kernel measured slower, 399 -> 416 us at 4096 tokens)
+        f32x16 s, s_odd;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) s[i] = s_odd[i] = 0.0f;
         const char* kt = &kbuf[buf][0] + krow_off;
 #pragma unroll
-        for (int g = 0; g < kG; ++g) {
-            const f32x4 kop = *(const lds_f32x4*)(kt + (kchunk((kSD / 4) * dq + 2 * g + hf, col) << 4));
+        for (int g = 0; g < kG; g += 2) {
+            const f32x4 kop0 = *(const lds_f32x4*)(kt + (kchunk((kSD / 4) * dq + 2 * g + hf, col) << 4));
+            const f32x4 kop1 = *(const lds_f32x4*)(kt + (kchunk((kSD / 4) * dq + 2 * (g + 1) + hf, col) << 4));
 #pragma unroll
-            for (int j = 0; j < 4; ++j) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kop[j], qop[g][j], s, 0, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kop0[j], qop[g][j], s, 0, 0, 0);
+                s_odd = __builtin_amdgcn_mfma_f32_32x32x2f32(kop1[j], qop[g + 1][j], s_odd, 0, 0, 0);
+            }
         }
+        s += s_odd;
         load_v(8);
         float* mine = &part[wave][0];
 #pragma unroll
