@@ -66,11 +66,10 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
     base = (const char*)(uintptr_t)ub;
     lds = __builtin_amdgcn_readfirstlane(lds);
     asm volatile(
-        "s_mov_b32 m0, %2\n\t"
         "s_nop 4\n\t"
         "global_load_lds_dwordx4 %0, %1"
         :
-        : "v"(voff), "s"(base), "s"(lds));
+        : "v"(voff), "s"(base), "{m0}"(lds));
 }
 
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)

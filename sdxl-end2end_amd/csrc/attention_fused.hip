@@ -12,14 +12,17 @@
 //   staged in LDS and shared by the workgroup's waves.
 //
 // Per wave and 32-key group (MFMA v_mfma_f32_32x32x16_{f16,bf16}):
-//   S^T[key][q] = K Q^T - m : A = K rows from LDS (16 B per lane); B = Q^T
-//                             from registers, pre-scaled by scale*log2(e); the
-//                             accumulator starts at -m (the softmax anchor),
-//                             so the MFMA emits exp2 arguments directly. The C
+//   S^T[key][q] = K Q^T - m/c : A = K rows from LDS (16 B per lane); B = Q^T
+//                             from registers as stored (exact products); the
+//                             accumulator starts at -m/c (m: the softmax
+//                             anchor in log2 units, c = scale*log2(e)). The C
 //                             layout puts one query per lane column: row sums
 //                             stay in-lane (plus one lane<->lane+32 exchange).
-//   P = exp2(S)              v_exp_f32, packed to fp16/bf16 (v_cvt_pk_*),
-//                             row sums in fp32 (before rounding).
+//   P = exp2(c S)            one fp32 multiply and v_exp_f32 per score, packed
+//                             to fp16/bf16 (v_cvt_pk_*), row sums in fp32
+//                             (before rounding). Q is not pre-scaled: rounding
+//                             q*c to fp16 costs 2^-12 of every score, which at
+//                             logits of a few tens exceeds the output bar.
 //   O^T[d][q] += V^T P^T    : A = V^T built with ds_read_b64_tr_b16 straight
 //                             from the row-major V tile (no transpose pass),
 //                             B = P^T from the registers holding P.
@@ -102,26 +105,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     }
 }
 
-// Multiplies eight packed fp16/bf16 values by c (round to nearest even).
-// Element-wise on a typed vector: writing dwords of a uint32 vector in a loop
-// while bit-casting its elements miscompiles with this toolchain.
-template <bool IsBf16>
-__device__ __forceinline__ i16x8 scale_operand(i16x8 x, float c) {
-    if constexpr (IsBf16) {
-        const bf16x8 v = __builtin_bit_cast(bf16x8, x);
-        bf16x8 r;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = (__bf16)((float)v[i] * c);
-        return __builtin_bit_cast(i16x8, r);
-    } else {
-        const f16x8 v = __builtin_bit_cast(f16x8, x);
-        f16x8 r;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = (_Float16)((float)v[i] * c);
-        return __builtin_bit_cast(i16x8, r);
-    }
-}
-
 // Sum of eight fp32 probabilities as a depth-3 tree. Plain fp32 adds: the
 // packed-dot (v_dot2) alternative shares issue resources with the matrix
 // cores and stalls them.
@@ -148,8 +131,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // with the s_waitcnt and s_barrier builtins around it, a transfer never
 // targets a buffer read in the same tile, and every tile begins with
 // vmcnt(0) + barrier before its buffers are read. M0 holds the wave-uniform
-// LDS destination; nothing else in this kernel uses M0 (the compiler treats it
-// as reserved and emits no M0 users here), so it is not listed as clobbered.
+// LDS destination, bound through an {m0} operand constraint so that the
+// compiler itself sets M0 and knows its value.
 __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint32_t lds) {
     // base and lds are wave-uniform by construction; readfirstlane makes that
     // explicit so that they are allocated to SGPRs as the instruction requires.
@@ -159,11 +142,10 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
     base = (const char*)(uintptr_t)ub;
     lds = __builtin_amdgcn_readfirstlane(lds);
     asm volatile(
-        "s_mov_b32 m0, %2\n\t"
         "s_nop 4\n\t"
         "global_load_lds_dwordx4 %0, %1"
         :
-        : "v"(voff), "s"(base), "s"(lds));
+        : "v"(voff), "s"(base), "{m0}"(lds));
 }
 
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
@@ -271,11 +253,11 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
 
     const int my_query = q0 + col;
 
+    // Scores leave the MFMA unscaled (exact products, fp32 sums); exp2
+    // arguments are c * S with c = scale*log2(e) > 0 (checked on the host).
     const float c = p.scale_log2;
-    // Q^T operand, pre-scaled by scale*log2(e) so that the MFMA yields scores
-    // directly in log2 units: lane holds dims 16*ks + 8*hf .. +7 of its query.
-    // The loads are issued here; the scaling (which waits for them) runs after
-    // the first K/V transfers are issued, so the two latencies overlap.
+    const float ic = p.inv_scale_log2;  // 1 / c, finite (checked on the host)
+    // Q^T operand as stored: lane holds dims 16*ks + 8*hf .. +7 of its query.
     i16x8 qop[4];
     if (my_query < p.q_seq) {
         const i16x8* qrow = (const i16x8*)(qbase + (int64_t)my_query * p.q_row_stride * elem);
@@ -285,10 +267,6 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) qop[ks] = i16x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    auto scale_q = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qop[ks] = scale_operand<IsBf16>(qop[ks], c);
-    };
 
     // Key range. Causal: keys beyond the block's last query are never visible.
     int n_keys = p.k_seq;
@@ -442,16 +420,17 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         }
     };
 
-    // Exact-maximum pass over scores sc[i0, i1) (relative to m_run): moves the
-    // anchor where needed (anchored rows move up only, unanchored rows take any
-    // finite maximum), rescales O and l and returns the shift every score
-    // computed against the old anchor must subtract.
+    // Exact-maximum pass over raw scores sc[i0, i1) (c * sc relative to
+    // m_run): moves the anchor where needed (anchored rows move up only,
+    // unanchored rows take any finite maximum), rescales O and l and returns
+    // the shift (log2 units) every exp2 argument formed against the old anchor
+    // must subtract; raw scores subtract shift / c (times ic = 1 / c).
     auto exact_max = [&](const f32x16& sc, int i0, int i1) __attribute__((always_inline)) -> float {
         float mx = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             if (i >= i0 && i < i1) mx = fmaxf(mx, sc[i]);
-        mx = xhalf_max(mx);
+        mx = xhalf_max(mx) * c;  // c > 0
         const bool move = anchored ? mx > 0.0f : mx > -__builtin_inff();
         const float shift = move ? mx : 0.0f;
         const float alpha = anchored ? __builtin_amdgcn_exp2f(-shift) : 0.0f;
@@ -462,7 +441,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
         l_run *= alpha;
         m_run += shift;
-        const float nm = -m_run;
+        const float nm = -m_run * ic;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float x = neg_m[i];
@@ -501,7 +480,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             }
         }
         if constexpr (kMasked || kExact) {
-            const float shift = exact_max(s_cur, 0, 16);
+            const float shift = exact_max(s_cur, 0, 16) * ic;
 #pragma unroll
             for (int i = 0; i < 16; ++i) s_cur[i] -= shift;
         }
@@ -516,12 +495,12 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // 1: QK1 | exp 0-3
         s_next = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
         __builtin_amdgcn_sched_barrier(0);
         // 2: QK2 | exp 4-7
         s_next = mfma32<IsBf16>(kop[1], qop[1], s_next);
 #pragma unroll
-        for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
         __builtin_amdgcn_sched_barrier(0);
         // 3: QK3 | pack + row sum of half 0, overflow check
         s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
@@ -532,14 +511,14 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
             // maximum over it and recompute. Rare.
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum)) != 0, 0)) {
-                const float shift = exact_max(s_cur, 0, 8);
+                const float shift = exact_max(s_cur, 0, 8) * ic;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     s_cur[i] -= shift;
                     s_next[i] -= shift;  // partial QK^T sum seeded with the old anchor
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+                for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
                 l_a = sum8(e);
@@ -550,14 +529,14 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // 4: QK4 | exp 8-11
         s_next = mfma32<IsBf16>(kop[3], qop[3], s_next);
 #pragma unroll
-        for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
         __builtin_amdgcn_sched_barrier(0);
         // 5: PV half 0, d 0-31 | exp 12-15; K operands of the group after next
         // (unconditional: stale data past the last tile is never used)
         const i16x8 p0 = __builtin_bit_cast(i16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
         acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
 #pragma unroll
-        for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+        for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
         if constexpr (kPrefetchK) load_k(kn2, g2, kop);
         __builtin_amdgcn_sched_barrier(0);
         // 6: PV half 0, d 32-63 | pack + row sum of half 1, overflow check
@@ -567,14 +546,14 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         float l_b = sum8(e + 8);
         if constexpr (kCheck) {
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum)) != 0, 0)) {
-                const float shift = exact_max(s_cur, 8, 16);
+                const float shift = exact_max(s_cur, 8, 16) * ic;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     s_cur[i] -= shift;
                     s_next[i] -= shift;
                 }
 #pragma unroll
-                for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
+                for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
 #pragma unroll
                 for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
                 l_b = sum8(e + 8);
@@ -603,7 +582,6 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // start instead of prefetching them a step earlier.
         issue_split(0, 0);
         issue_split(1, -1);
-        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], khalf, kop);
@@ -634,7 +612,6 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // tile (as the key-split kind); one barrier per tile step for all.
         issue_mixed(0, 0);
         issue_mixed(1, -1);
-        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], khalf, kop);
@@ -684,7 +661,6 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     if (n_tiles > 0) {
         issue(0, 0);
         issue(1, -1);
-        scale_q();
         wait_vmem_all();
         __syncthreads();
         load_k(kring[0], 0, kop);

@@ -34,6 +34,7 @@ struct FusedAttentionParams {
     int32_t q_blocks;      // filled by the launcher
     int32_t total_blocks;  // filled by the launcher
     float scale_log2;      // softmax scale * log2(e)
+    float inv_scale_log2;  // 1 / scale_log2 (finite)
     int32_t whole_units;   // filled by the launcher: 128-row workgroups (ids first)
     int32_t split_units;   // filled by the launcher: 64-row key-split workgroups
     int32_t short_chunk_blocks;  // filled by the short-key launcher: 32-row blocks per workgroup

@@ -201,6 +201,12 @@ sdxl_status sdxl_attn_fwd(const sdxl_attn_desc* d, const void* q, const void* k,
         }
     }
 
+    // The fused kernels form exp2 arguments as c * S and shift raw scores by
+    // m / c (c = scale * log2 e); a scale so small that 1 / c overflows runs
+    // on the per-row kernel, which multiplies by the scale directly.
+    const float scale_log2 = scale * 1.4426950408889634f;
+    if (backend != SDXL_ATTN_WARP_ONLINE && !std::isfinite(1.0f / scale_log2)) backend = SDXL_ATTN_WARP_ONLINE;
+
     hipError_t err;
     if (backend == SDXL_ATTN_WARP_ONLINE) {
         sdxl_hip::OnlineAttentionParams p{};
@@ -227,7 +233,8 @@ sdxl_status sdxl_attn_fwd(const sdxl_attn_desc* d, const void* q, const void* k,
         p.o_row_stride = eff_stride(d->o_row_stride, width);
         p.batch = (int32_t)d->batch; p.q_seq = (int32_t)d->q_seq; p.k_seq = (int32_t)d->k_seq;
         p.heads = (int32_t)d->heads; p.causal = d->causal != 0;
-        p.scale_log2 = scale * 1.4426950408889634f;
+        p.scale_log2 = scale_log2;
+        p.inv_scale_log2 = 1.0f / scale_log2;
         const int64_t blocks = ((d->q_seq + sdxl_hip::fused_attention_block_queries() - 1) /
                                 sdxl_hip::fused_attention_block_queries()) * d->heads * d->batch;
         if (blocks > INT32_MAX) return fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_attn: grid too large");
