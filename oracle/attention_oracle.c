@@ -415,3 +415,133 @@ void oracle_quantize_e4m3_rows(const float* W, size_t rows, size_t cols, uint8_t
     for (size_t r = 0; r < rows; ++r)
         for (size_t c = 0; c < cols; ++c) q[r * cols + c] = oracle_float_to_e4m3(W[r * cols + c] / scales[r]);
 }
+
+/* ------------------------------------------------------------------ */
+/* The transformer block's two attention halves, in the reference's   */
+/* block order (src/unet.cpp:495-512), FP32 throughout.                */
+/* ------------------------------------------------------------------ */
+
+/* Row-parallel helper: fn(ctx, r0, r1) over [0, n) split in `threads`
+ * contiguous ranges. Every row is computed as in the single-threaded loop. */
+typedef void (*oracle_rows_fn)(void* ctx, size_t r0, size_t r1);
+typedef struct { oracle_rows_fn fn; void* ctx; size_t r0, r1; } rows_job;
+
+static void* rows_worker(void* arg) {
+    rows_job* j = (rows_job*)arg;
+    j->fn(j->ctx, j->r0, j->r1);
+    return NULL;
+}
+
+static void parallel_rows(oracle_rows_fn fn, void* ctx, size_t n, int threads) {
+    if (threads < 1) threads = 1;
+    if ((size_t)threads > n) threads = n > 0 ? (int)n : 1;
+    if (threads == 1) { fn(ctx, 0, n); return; }
+    pthread_t* ids = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    rows_job* jobs = (rows_job*)malloc(sizeof(rows_job) * (size_t)threads);
+    for (int t = 0; t < threads; ++t) {
+        rows_job j = {fn, ctx, n * (size_t)t / (size_t)threads, n * (size_t)(t + 1) / (size_t)threads};
+        jobs[t] = j;
+        pthread_create(&ids[t], NULL, rows_worker, &jobs[t]);
+    }
+    for (int t = 0; t < threads; ++t) pthread_join(ids[t], NULL);
+    free(ids);
+    free(jobs);
+}
+
+typedef struct { const float *x, *W, *bias; float* y; size_t in, out; } linear_ctx;
+
+static void linear_rows(void* c, size_t r0, size_t r1) {
+    linear_ctx* l = (linear_ctx*)c;
+    oracle_linear(l->x + r0 * l->in, l->W, l->bias, l->y + r0 * l->out, r1 - r0, l->in, l->out);
+}
+
+/* y[rows] = x[rows] W^T + bias, rows split over threads (same sums as oracle_linear). */
+static void linear_mt(const float* x, const float* W, const float* bias, float* y, size_t rows, size_t in,
+                      size_t out, int threads) {
+    linear_ctx c = {x, W, bias, y, in, out};
+    parallel_rows(linear_rows, &c, rows, threads);
+}
+
+typedef struct {
+    const float *q, *k, *v;
+    float* o;
+    size_t Sq, Sk, H, D, q_begin, q_end;
+    float scale;
+} attn_rows_ctx;
+
+static void attention_task_rows(void* c, size_t t0, size_t t1) {
+    attn_rows_ctx* a = (attn_rows_ctx*)c;
+    float* score = (float*)malloc((a->Sk + 1) * sizeof(float));
+    float* prob = (float*)malloc((a->Sk + 1) * sizeof(float));
+    for (size_t t = t0; t < t1; ++t)
+        attention_rows(a->q, a->k, a->v, a->o, t / a->H, t % a->H, a->q_begin, a->q_end, a->Sq, a->Sk, a->H,
+                       a->D, a->scale, NULL, 0, score, prob);
+    free(score);
+    free(prob);
+}
+
+/* Shared tail of both halves, for query rows [q_begin, q_end) of every batch:
+ * attention of q against k/v (full_attention, src/unet.cpp:440-481), then
+ * linear_3d with the output weight and bias, then add_in_place onto the
+ * hidden state (src/unet.cpp:505-506, :511-512): y = x + out. */
+static void attention_half_tail(const float* x, const float* q, const float* k, const float* v,
+                                const float* wo, const float* bo, size_t B, size_t S, size_t Sk, size_t W,
+                                size_t heads, size_t q_begin, size_t q_end, float* y, int threads) {
+    const size_t D = W / heads, rows = q_end - q_begin;
+    float* attn = (float*)calloc(B * S * W + 1, sizeof(float));
+    attn_rows_ctx ac = {q, k, v, attn, S, Sk, heads, D, q_begin, q_end, 1.0f / sqrtf((float)D)};
+    parallel_rows(attention_task_rows, &ac, B * heads, threads);
+    float* proj = (float*)malloc(rows * W * sizeof(float) + 4);
+    for (size_t b = 0; b < B; ++b) {
+        const size_t r = b * S + q_begin;
+        linear_mt(attn + r * W, wo, bo, proj, rows, W, W, threads);
+        for (size_t i = 0; i < rows * W; ++i) y[r * W + i] = x[r * W + i] + proj[i];
+    }
+    free(proj);
+    free(attn);
+}
+
+/* Self-attention half of UNet::transformer_block (src/unet.cpp:500-506):
+ * norm1 = layer_norm(x); q, k, v = three separate bias-free linear_3d of
+ * norm1 (weights [W, W], [out, in]); attn = full_attention(q, k, v, heads);
+ * attn = linear_3d(attn, wo, bo); x += attn. Computes the block's output for
+ * query rows [q_begin, q_end) of every batch into y ([B, S, W]; other rows
+ * untouched). Keys and values are computed for every row. */
+void oracle_attn_sublayer(const float* x, const float* gamma, const float* beta, const float* wq,
+                          const float* wk, const float* wv, const float* wo, const float* bo, size_t B,
+                          size_t S, size_t W, size_t heads, size_t q_begin, size_t q_end, float* y,
+                          int threads) {
+    const size_t n = B * S * W, rows = q_end - q_begin;
+    float* norm = (float*)malloc(n * sizeof(float) + 4);
+    float* q = (float*)calloc(n + 1, sizeof(float));
+    float* k = (float*)malloc(n * sizeof(float) + 4);
+    float* v = (float*)malloc(n * sizeof(float) + 4);
+    oracle_layer_norm(x, gamma, beta, norm, B * S, W, 1.0e-5f);
+    for (size_t b = 0; b < B; ++b)
+        linear_mt(norm + (b * S + q_begin) * W, wq, NULL, q + (b * S + q_begin) * W, rows, W, W, threads);
+    linear_mt(norm, wk, NULL, k, B * S, W, W, threads);
+    linear_mt(norm, wv, NULL, v, B * S, W, W, threads);
+    attention_half_tail(x, q, k, v, wo, bo, B, S, S, W, heads, q_begin, q_end, y, threads);
+    free(norm); free(q); free(k); free(v);
+}
+
+/* Cross-attention half (src/unet.cpp:508-512): norm2 = layer_norm(x); q from
+ * norm2; k, v = bias-free linear_3d of the context ctx [B, L, C] with
+ * weights [W, C]; then as the self half. */
+void oracle_cross_attn_sublayer(const float* x, const float* gamma, const float* beta, const float* wq,
+                                const float* ctx, const float* wk, const float* wv, const float* wo,
+                                const float* bo, size_t B, size_t S, size_t W, size_t L, size_t C,
+                                size_t heads, size_t q_begin, size_t q_end, float* y, int threads) {
+    const size_t n = B * S * W, rows = q_end - q_begin;
+    float* norm = (float*)malloc(n * sizeof(float) + 4);
+    float* q = (float*)calloc(n + 1, sizeof(float));
+    float* k = (float*)malloc(B * L * W * sizeof(float) + 4);
+    float* v = (float*)malloc(B * L * W * sizeof(float) + 4);
+    oracle_layer_norm(x, gamma, beta, norm, B * S, W, 1.0e-5f);
+    for (size_t b = 0; b < B; ++b)
+        linear_mt(norm + (b * S + q_begin) * W, wq, NULL, q + (b * S + q_begin) * W, rows, W, W, threads);
+    linear_mt(ctx, wk, NULL, k, B * L, C, W, threads);
+    linear_mt(ctx, wv, NULL, v, B * L, C, W, threads);
+    attention_half_tail(x, q, k, v, wo, bo, B, S, L, W, heads, q_begin, q_end, y, threads);
+    free(norm); free(q); free(k); free(v);
+}

@@ -71,6 +71,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_quantize_e4m3_rows.restype = None
         L.oracle_quantize_e4m3_rows.argtypes = [_f32p, _sz, _sz,
                                                 np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS"), _f32p]
+        L.oracle_attn_sublayer.restype = None
+        L.oracle_attn_sublayer.argtypes = [_f32p] * 8 + [_sz] * 6 + [_f32p, ctypes.c_int]
+        L.oracle_cross_attn_sublayer.restype = None
+        L.oracle_cross_attn_sublayer.argtypes = [_f32p] * 9 + [_sz] * 8 + [_f32p, ctypes.c_int]
         _lib = L
     return _lib
 
@@ -90,6 +94,9 @@ def ref() -> ctypes.CDLL:
         R.ref_layer_norm.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, ctypes.c_float]
         R.ref_linear.restype = ctypes.c_int
         R.ref_linear.argtypes = [_f32p, _f32p, ctypes.c_void_p, _f32p, _sz, _sz, _sz]
+        R.ref_transformer_block.restype = ctypes.c_int
+        R.ref_transformer_block.argtypes = [_f32p, _f32p, ctypes.POINTER(ctypes.c_void_p), _f32p,
+                                            _sz, _sz, _sz, _sz, _sz, _sz]
         _ref = R
     return _ref
 
@@ -233,3 +240,54 @@ def error_stats(candidate, reference):
         return 0.0, 0.0, 0.0
     a = np.abs(d)
     return float(a.max()), float(a.mean()), float(np.sqrt((d * d).mean()))
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def attn_sublayer(x, gamma, beta, wq, wk, wv, wo, bo, heads: int, q_begin: int = 0, q_end=None,
+                  threads: int = 1) -> np.ndarray:
+    """Self-attention half of the reference's transformer block (src/unet.cpp:500-506) in FP32:
+    x [B, S, W] -> x + linear(full_attention(LN(x) Wq^T, LN(x) Wk^T, LN(x) Wv^T), Wo, bo).
+    Returns [B, S, W] with rows [q_begin, q_end) filled (others zero)."""
+    x = _c32(x)
+    B, S, W = x.shape
+    q_end = S if q_end is None else q_end
+    y = np.zeros_like(x)
+    lib().oracle_attn_sublayer(x, _c32(gamma), _c32(beta), _c32(wq), _c32(wk), _c32(wv), _c32(wo), _c32(bo),
+                               B, S, W, heads, q_begin, q_end, y, threads)
+    return y
+
+
+def cross_attn_sublayer(x, gamma, beta, wq, ctx, wk, wv, wo, bo, heads: int, q_begin: int = 0, q_end=None,
+                        threads: int = 1) -> np.ndarray:
+    """Cross-attention half (src/unet.cpp:508-512): keys/values from ctx [B, L, C] through
+    wk, wv [W, C]. Same conventions as attn_sublayer."""
+    x = _c32(x)
+    ctx = _c32(ctx)
+    B, S, W = x.shape
+    L, C = ctx.shape[1], ctx.shape[2]
+    q_end = S if q_end is None else q_end
+    y = np.zeros_like(x)
+    lib().oracle_cross_attn_sublayer(x, _c32(gamma), _c32(beta), _c32(wq), ctx, _c32(wk), _c32(wv), _c32(wo),
+                                     _c32(bo), B, S, W, L, C, heads, q_begin, q_end, y, threads)
+    return y
+
+
+def ref_transformer_block(x, ctx, weights, heads: int) -> np.ndarray:
+    """The reference's own UNet transformer_block (src/unet.cpp:495-523) on a block of its
+    declared SDXL graph, parameters bound to the 20 arrays of `weights` (reference order:
+    norm1 w/b, attn1 q/k/v/out w, out b, norm2 w/b, attn2 q/k/v/out w, out b, norm3 w/b,
+    ff0 w/b, ff2 w/b). Container only (needs oracle/_ref)."""
+    x = _c32(x)
+    ctx = _c32(ctx)
+    B, S, W = x.shape
+    ws = [_c32(w) for w in weights]
+    ptrs = (ctypes.c_void_p * len(ws))(*[w.ctypes.data for w in ws])
+    y = np.empty_like(x)
+    rc = ref().ref_transformer_block(x, ctx, ptrs, y, B, S, W, ctx.shape[1], ctx.shape[2], heads)
+    if rc != 0:
+        raise RuntimeError(f"ref_transformer_block failed ({rc})")
+    return y
+

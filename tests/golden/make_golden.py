@@ -15,6 +15,13 @@ case and the reference's outputs. Input recipes:
   tail        seeded N(0,1) fp16, q [1, 96, 64], k/v [1, 200, 64], 1 head
   layer_norm  x N(0,1) [8, 640], w N(1, 0.1), b N(0, 0.1), eps 1e-5
   linear      x N(0,1) [8, 64], W N(0, 0.02) [48, 64], bias N(0, 0.1)
+  block_self  the reference's own UNet transformer_block (src/unet.cpp:495-523) on a level-1 block of
+              its declared SDXL graph (640 channels, 10 heads, context 2048), x [1, 40, 640], with the
+              cross half's output projection and the feed-forward zeroed: output = x + self half
+  block_cross the same on a level-2 block (1280 channels, 20 heads), x [1, 24, 1280], context
+              [1, 77, 2048], with the self half's output projection and the feed-forward zeroed:
+              output = x + cross half
+              (inputs of both from block_inputs() below, seeded; only the outputs are stored)
 
 Usage: python tests/golden/make_golden.py
 """
@@ -46,6 +53,33 @@ def ref_attention(q, k, v, heads):
                                          W // heads)
     assert rc == 0
     return out
+
+
+def block_inputs(kind):
+    """Seeded inputs of the transformer-block cases: (x, ctx, weights in the reference's parameter
+    order, heads, the half's own parameters (gamma, beta, wq, wk, wv, wo, bo))."""
+    if kind == "block_self":
+        B, S, W, H, seed = 1, 40, 640, 10, 50
+    else:
+        B, S, W, H, seed = 1, 24, 1280, 20, 60
+    L, C = 77, 2048
+    x = oracle.normal_f32(seed, (B, S, W))
+    ctx = oracle.normal_f32(seed + 1, (B, L, C))
+    gamma = (1.0 + oracle.normal_f32(seed + 2, (W,), 0.1)).astype(np.float32)
+    beta = oracle.normal_f32(seed + 3, (W,), 0.1)
+    wq, wo = (oracle.normal_f32(seed + 4 + i, (W, W), 0.05) for i in range(2))
+    bo = oracle.normal_f32(seed + 6, (W,), 0.05)
+    kv_in = W if kind == "block_self" else C
+    wk, wv = (oracle.normal_f32(seed + 7 + i, (W, kv_in), 0.05 if kind == "block_self" else 0.02)
+              for i in range(2))
+    one, zero = np.ones(W, np.float32), np.zeros(W, np.float32)
+    z = lambda *shape: np.zeros(shape, np.float32)
+    ff = [one, zero, z(8 * W, W), z(8 * W), z(W, 4 * W), zero]
+    if kind == "block_self":
+        weights = [gamma, beta, wq, wk, wv, wo, bo, one, zero, z(W, W), z(W, C), z(W, C), z(W, W), zero] + ff
+    else:
+        weights = [one, zero, z(W, W), z(W, W), z(W, W), z(W, W), zero, gamma, beta, wq, wk, wv, wo, bo] + ff
+    return x, ctx, weights, H, (gamma, beta, wq, wk, wv, wo, bo)
 
 
 def main():
@@ -98,6 +132,10 @@ def main():
     y = np.empty((8, 48), np.float32)
     assert oracle.ref().ref_linear(x, W, bias.ctypes.data, y, 8, 64, 48) == 0
     data.update(linear_x=x, linear_w=W, linear_b=bias, linear_out=y)
+
+    for kind in ("block_self", "block_cross"):
+        x, ctx, weights, heads, _ = block_inputs(kind)
+        data[f"{kind}_out"] = oracle.ref_transformer_block(x, ctx, weights, heads)
 
     out = os.path.join(HERE, "attention_golden.npz")
     np.savez_compressed(out, **data)

@@ -13,12 +13,11 @@ import pytest
 
 import oracle
 import sdxl_hip as sh
+from parity import MAX_ABS, MEAN_ABS, assert_parity, assert_parity_f16_out
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-MAX_ABS = 2e-3
-MEAN_ABS = 2e-4
 THREADS = min(16, os.cpu_count() or 1)
 DEV = "cuda:0"
 
@@ -38,12 +37,6 @@ def run(qb, kb, vb, heads, backend=sh.AUTO, **kw):
     return from_dev(out)
 
 
-def assert_parity(got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, label=""):
-    mx, mean, _ = oracle.error_stats(got, ref)
-    print(f"{label}: max_abs={mx:.3e} mean_abs={mean:.3e}", flush=True)
-    assert np.isfinite(got).all(), label
-    assert mx <= max_abs, (label, mx)
-    assert mean <= mean_abs, (label, mean)
 
 
 def seeded(seed, B, S, W):
@@ -541,28 +534,6 @@ def _large_logit_inputs(kind, B, Sq, Sk, H, seed):
         kf.reshape(B, Sk, H, 64)[:, late, :, 0] = 64.0
         q, k = oracle.f32_to_f16_bits(qf), oracle.f32_to_f16_bits(kf)
     return q, k, v
-
-
-def half_ulp_f16(x):
-    """Half the fp16 spacing at |x| (the rounding error of a correctly rounded fp16 output)."""
-    a = np.maximum(np.abs(np.asarray(x, np.float64)), 2.0 ** -14)
-    return np.ldexp(1.0, np.floor(np.log2(a)).astype(np.int64) - 11)
-
-
-def assert_parity_f16_out(got, ref, max_abs=MAX_ABS, mean_abs=MEAN_ABS, label=""):
-    """The parity bar with the fp16 output's own final rounding allowed on top of the max-abs bar.
-    Peaked softmaxes return single value rows, |o| up to ~4.5 here, where half an fp16 ulp is
-    9.8e-4 ([2, 4)) or 1.95e-3 ([4, 8)): no fp16 output can be closer to the fp32 oracle than
-    that. Below |o| = 1 the allowance is at most 2.4e-4."""
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    err = np.abs(got - ref)
-    excess = (err - half_ulp_f16(ref)).max() if err.size else 0.0
-    print(f"{label}: max_abs={err.max():.3e} beyond output rounding={excess:.3e} mean_abs={err.mean():.3e}"
-          f" max|ref|={np.abs(ref).max():.2f}", flush=True)
-    assert np.isfinite(got).all(), label
-    assert excess <= max_abs, (label, excess)
-    assert err.mean() <= mean_abs, (label, err.mean())
 
 
 def _check_rows_and_torch(got, qb, kb, vb, H, label, rows=None, max_abs=MAX_ABS, mean_abs=MEAN_ABS):

@@ -224,7 +224,76 @@ def test_linear_matches_reference_golden_and_numpy():
     np.testing.assert_allclose(got, x.astype(np.float64) @ W.T.astype(np.float64) + b, atol=1e-5)
 
 
+# ------------------------------------------------------------------ the block's attention halves
+
+def _block_inputs(kind):
+    import importlib.util
+    import os
+    spec = importlib.util.spec_from_file_location(
+        "make_golden", os.path.join(os.path.dirname(__file__), "golden", "make_golden.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.block_inputs(kind)
+
+
+def test_attn_sublayer_matches_reference_transformer_block_golden():
+    """Self half (src/unet.cpp:500-506) bit-exact to the reference's own transformer_block output
+    (cross half and feed-forward zeroed there), all rows and a row subset."""
+    x, ctx, _, heads, (g, b, wq, wk, wv, wo, bo) = _block_inputs("block_self")
+    want = GOLDEN["block_self_out"]
+    got = oracle.attn_sublayer(x, g, b, wq, wk, wv, wo, bo, heads, threads=4)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    part = oracle.attn_sublayer(x, g, b, wq, wk, wv, wo, bo, heads, q_begin=7, q_end=19, threads=3)
+    assert (part[:, 7:19].view(np.uint32) == want[:, 7:19].view(np.uint32)).all()
+    assert np.abs(want - x).max() > 0.1  # the half contributes
+
+
+def test_cross_attn_sublayer_matches_reference_transformer_block_golden():
+    """Cross half (src/unet.cpp:508-512), level-2 block: bit-exact to the reference's own output."""
+    x, ctx, _, heads, (g, b, wq, wk, wv, wo, bo) = _block_inputs("block_cross")
+    want = GOLDEN["block_cross_out"]
+    got = oracle.cross_attn_sublayer(x, g, b, wq, ctx, wk, wv, wo, bo, heads, threads=4)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    assert np.abs(want - x).max() > 0.1
+
+
+def test_attn_sublayer_equals_composition_of_pinned_pieces():
+    """The half restated from the (separately pinned) LayerNorm, linear and attention in the
+    reference's block order, on a ragged small case."""
+    B, S, W, H = 2, 37, 128, 2
+    x = oracle.normal_f32(70, (B, S, W))
+    g, b = 1 + oracle.normal_f32(71, (W,), 0.1), oracle.normal_f32(72, (W,), 0.1)
+    wq, wk, wv, wo = (oracle.normal_f32(73 + i, (W, W), 0.1) for i in range(4))
+    bo = oracle.normal_f32(77, (W,), 0.1)
+    n = oracle.layer_norm(x, g, b)
+    attn = oracle.attention_f32(oracle.linear(n, wq), oracle.linear(n, wk), oracle.linear(n, wv), H)
+    want = x + oracle.linear(attn, wo, bo)
+    got = oracle.attn_sublayer(x, g, b, wq, wk, wv, wo, bo, H, threads=2)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
 # ------------------------------------------------------------------ live reference (container only)
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no /root/reference)")
+def test_block_halves_equal_live_reference_block():
+    """Fresh seeds through the reference's transformer_block (level 1, both halves live at once:
+    the oracle's self half followed by its cross half on the result, feed-forward zeroed)."""
+    B, S, W, H, L, C = 2, 19, 640, 10, 77, 2048
+    x = oracle.normal_f32(80, (B, S, W))
+    ctx = oracle.normal_f32(81, (B, L, C))
+    p1 = [1 + oracle.normal_f32(82, (W,), 0.1), oracle.normal_f32(83, (W,), 0.1)] + \
+         [oracle.normal_f32(84 + i, (W, W), 0.05) for i in range(4)] + [oracle.normal_f32(88, (W,), 0.05)]
+    p2 = [1 + oracle.normal_f32(89, (W,), 0.1), oracle.normal_f32(90, (W,), 0.1), oracle.normal_f32(91, (W, W), 0.05),
+          oracle.normal_f32(92, (W, C), 0.02), oracle.normal_f32(93, (W, C), 0.02), oracle.normal_f32(94, (W, W), 0.05),
+          oracle.normal_f32(95, (W,), 0.05)]
+    z = lambda *shape: np.zeros(shape, np.float32)
+    ff = [np.ones(W, np.float32), z(W), z(8 * W, W), z(8 * W), z(W, 4 * W), z(W)]
+    want = oracle.ref_transformer_block(x, ctx, p1 + p2 + ff, H)
+    h1 = oracle.attn_sublayer(x, *p1, H, threads=4)
+    got = oracle.cross_attn_sublayer(h1, p2[0], p2[1], p2[2], ctx, *p2[3:], H, threads=4)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+
+
 
 @pytest.mark.skipif(not oracle.ref_available(), reason="oracle/_ref not built (no /root/reference)")
 @pytest.mark.parametrize("shape", [(1, 64, 64, 1, 64), (2, 37, 77, 3, 64), (1, 20, 200, 2, 64), (1, 3, 5, 1, 512)])
