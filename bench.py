@@ -25,6 +25,7 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "sdxl-end2end_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 METRIC = "attention TFLOP/s + µs/call, SDXL 4096-tok self-attn b2 h10 d64 fp16"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
@@ -43,22 +44,39 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
     ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae) and exit")
-    ap.add_argument("--ceiling", action="store_true",
-                    help="profiling aid: power-limited ceilings (hipBLASLt fp16 GEMM and the c3 attention on "
-                         "random vs zero operands) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
 
 
-def make_inputs(torch, B, Sq, Sk, H, seed):
-    g = torch.Generator(device="cuda:0")
-    g.manual_seed(seed)
+def make_inputs(torch, B, Sq, Sk, H, seed, host=False):
+    """Seeded N(0,1) fp16 Q, K, V ([B, S, H*64]) from the documented generator (SplitMix64 ->
+    Box-Muller, rounded to nearest even; q = seed, k = seed + 1, v = seed + 2), copied to HBM.
+    host=True also returns the fp16 bit arrays (for the output check)."""
+    import numpy as np
+    import oracle
     W = H * 64
-    q = torch.randn(B, Sq, W, device="cuda:0", generator=g).half()
-    k = torch.randn(B, Sk, W, device="cuda:0", generator=g).half()
-    v = torch.randn(B, Sk, W, device="cuda:0", generator=g).half()
-    return q, k, v
+    bits = (oracle.normal_f16(seed, (B, Sq, W)), oracle.normal_f16(seed + 1, (B, Sk, W)),
+            oracle.normal_f16(seed + 2, (B, Sk, W)))
+    dev = tuple(torch.from_numpy(b.view(np.int16)).to("cuda:0").view(torch.float16) for b in bits)
+    return (dev, bits) if host else dev
+
+
+def check_output(out, bits, heads, rows=((0, 16), (2040, 2056), (4080, 4096))):
+    """The timed output against the oracle (FP32 restatement of src/unet.cpp:440-481) on row
+    subsets, outside the timed region: max / mean absolute error."""
+    import numpy as np
+    import oracle
+    got = out.float().cpu().numpy()
+    qb, kb, vb = bits
+    worst, total, n = 0.0, 0.0, 0
+    for r0, r1 in rows:
+        ref = oracle.attention_f16_rows(qb, kb, vb, heads, r0, r1)
+        d = np.abs(got[:, r0:r1].astype(np.float64) - ref[:, r0:r1])
+        worst, total, n = max(worst, float(d.max())), total + float(d.sum()), n + d.size
+    return {"oracle": "FP32 restatement of src/unet.cpp:440-481", "rows": [list(r) for r in rows],
+            "max_abs": worst, "mean_abs": total / n, "bar": {"max_abs": 2e-3, "mean_abs": 2e-4},
+            "pass": worst <= 2e-3 and total / n <= 2e-4}
 
 
 def time_calls(torch, sh, q, k, v, heads, steps, warmup):
@@ -247,31 +265,6 @@ def bench_cross_sublayer(torch, sh, steps=50, warmup=5):
     return out
 
 
-def ceiling(torch, sh):
-    """Data-dependent throughput: the same instruction streams on N(0,1) operands and on a zero
-    operand. MFMA power scales with operand toggling; on random data the device lowers its clock."""
-    res = {}
-    n = 8192
-    a = torch.randn(n, n, device="cuda:0", dtype=torch.float16)
-    b = torch.randn(n, n, device="cuda:0", dtype=torch.float16)
-    for label in ("randn", "zero_b"):
-        if label == "zero_b":
-            b.zero_()
-        ms = time_fn(torch, lambda: torch.matmul(a, b), 10, 3, reps=5)
-        res[f"hipblaslt_gemm_{n}_{label}_tflops"] = round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)
-    del a, b
-    B, Sq, Sk, H = 2, 4096, 4096, 10
-    q, k, v = make_inputs(torch, B, Sq, Sk, H, 1234)
-    o = torch.empty_like(q)
-    for label in ("randn", "zero_q"):
-        if label == "zero_q":
-            q.zero_()
-        ms = time_fn(torch, lambda: sh.attention(q, k, v, H, out=o), 30, 3)
-        res[f"attention_c3_{label}_us"] = round(ms * 1e3, 2)
-        res[f"attention_c3_{label}_tflops"] = round(sh.attention_flops(B, H, Sq, Sk) / (ms * 1e-3) / 1e12, 1)
-    return res
-
-
 def read_traffic():
     """HBM bytes per launch of the headline kernel from the committed rocprofv3 --pmc summary."""
     try:
@@ -283,34 +276,62 @@ def read_traffic():
     return None
 
 
-def cpu_baseline(q, k, v, heads_sample=6):
-    """The reference's single-threaded full_attention (src/unet.cpp:440-481) on batch 0,
-    heads 0..heads_sample-1, all query rows of the headline shape."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(bits, heads, threads, single_pairs=4):
+    """The reference's own full_attention (src/unet.cpp:440-481, compiled from its sources into
+    oracle/_ref/libref_attention.so; the oracle's restatement when that is absent) on the host
+    cores, on the headline workload:
+      * all cores: `threads` workers over the B*H (batch, head) pairs of the whole workload, each
+        pair one call of the single-threaded function (ctypes releases the GIL);
+      * one thread: the first `single_pairs` pairs, as the reference runs it."""
     import numpy as np
     import oracle
-    W = 64 * heads_sample
-    qs = np.ascontiguousarray(q[0:1, :, :W].float().cpu().numpy())
-    ks = np.ascontiguousarray(k[0:1, :, :W].float().cpu().numpy())
-    vs = np.ascontiguousarray(v[0:1, :, :W].float().cpu().numpy())
-    out = np.zeros_like(qs)
-    Sq, Sk = qs.shape[1], ks.shape[1]
-    if oracle.ref_available():
-        kind = "reference"
-        t0 = time.perf_counter()
-        rc = oracle.ref().ref_full_attention(qs, ks, vs, out, 1, Sq, Sk, heads_sample, 64)
-        dt = time.perf_counter() - t0
-        assert rc == 0
-    else:
-        kind = "port"
-        t0 = time.perf_counter()
-        out = oracle.attention_f32(qs, ks, vs, heads_sample, threads=1)
-        dt = time.perf_counter() - t0
-    flops = 4.0 * heads_sample * Sq * Sk * 64
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": kind,
-            "sample": f"batch 0, heads 0-{heads_sample - 1} of [2,10,{Sq},64] x {Sk} keys "
-                      f"({heads_sample}/20 of the workload), single thread, {dt:.2f} s",
-            "seconds": round(dt, 3)}
+    from concurrent.futures import ThreadPoolExecutor
+    qb, kb, vb = bits
+    B, Sq, W = qb.shape
+    Sk = kb.shape[1]
+    f32 = lambda x: oracle.f16_bits_to_f32(x)
+    q, k, v = f32(qb), f32(kb), f32(vb)
+    pairs = [(b, h) for b in range(B) for h in range(heads)]
+    slices = {p: tuple(np.ascontiguousarray(t[p[0]:p[0] + 1, :, 64 * p[1]:64 * (p[1] + 1)]) for t in (q, k, v))
+              for p in pairs}
+    kind = "reference" if oracle.ref_available() else "port"
+
+    def one(p):
+        qs, ks, vs = slices[p]
+        out = np.zeros_like(qs)
+        if kind == "reference":
+            assert oracle.ref().ref_full_attention(qs, ks, vs, out, 1, Sq, Sk, 1, 64) == 0
+        else:
+            out = oracle.attention_f32(qs, ks, vs, 1)
+        return out
+
+    flops_pair = 4.0 * Sq * Sk * 64
+    t0 = time.perf_counter()
+    for p in pairs[:single_pairs]:
+        one(p)
+    t_single = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(one, pairs))
+    t_all = time.perf_counter() - t0
+    return {"value": round(flops_pair * len(pairs) / t_all / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "kind": kind, "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
+            "sample": f"the whole workload: {len(pairs)} (batch, head) pairs of [2,10,{Sq},64] x {Sk} keys "
+                      f"over {threads} threads, {t_all:.2f} s (mode ii: all cores over (b, h))",
+            "us_per_call": round(t_all * 1e6, 1),
+            "single_thread": {"value": round(flops_pair * single_pairs / t_single / 1e12, 6), "unit": "TFLOP/s",
+                              "sample": f"{single_pairs} of {len(pairs)} (batch, head) pairs, one thread, "
+                                        f"{t_single:.2f} s (mode i: the reference's own loop)"}}
 
 
 def main():
@@ -344,9 +365,6 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         return
-    if args.ceiling:
-        print(json.dumps(ceiling(torch, sh)), flush=True)
-        return
     if args.only == "c4":
         print(json.dumps(bench_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
@@ -366,11 +384,12 @@ def main():
         return
 
     B, Sq, Sk, H, _ = configs["c3"]
-    q, k, v = make_inputs(torch, B, Sq, Sk, H, 1234)
+    (q, k, v), bits = make_inputs(torch, B, Sq, Sk, H, 1234, host=True)
     desc = sh.make_desc(B, Sq, Sk, H)
     backend = sh.load().sdxl_attn_kernel_name(sh.resolve_backend(desc)).decode()
     torch.cuda.synchronize()
-    wall_ms, kernel_ms, _ = time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
+    wall_ms, kernel_ms, out = time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
+    parity = check_output(out, bits, H)
     flops = sh.attention_flops(B, H, Sq, Sk)
     value = flops / (wall_ms * 1e-3) / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
@@ -388,7 +407,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded N(0,1) fp16 Q/K/V resident in HBM)",
+        "data": "synthetic: seeded N(0,1) fp16 Q/K/V (SplitMix64 + Box-Muller, q/k/v seeds 1234/1235/1236) "
+                "resident in HBM",
         "config": {"workload": "SDXL level-1 self-attention, Q,K,V fp16 [2,10,4096,64] (BSHD [2,4096,640]), "
                                "scale 1/8, non-causal", "batch": B, "heads": H, "q_seq": Sq, "k_seq": Sk,
                    "head_dim": 64, "backend": backend},
@@ -398,6 +418,8 @@ def main():
                      "algorithmic_flops_per_launch": flops,
                      "algorithmic_bytes_per_launch": sh.attention_bytes(B, H, Sq, Sk)},
     }
+
+    result["parity"] = parity
 
     if not args.no_secondary:
         sec = {}
@@ -424,7 +446,7 @@ def main():
         result["secondary"] = sec
 
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(q, k, v)
+        result["cpu_baseline"] = cpu_baseline(bits, H, threads=min(16, os.cpu_count() or 1))
     else:
         result["cpu_baseline"] = None
 
