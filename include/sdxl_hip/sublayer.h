@@ -114,6 +114,22 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* desc, const void* x, co
                                const void* w_out, const void* b_out, void* y, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of sdxl_attn_sublayer. No counterpart in the reference:
+ * for callers that cannot allocate device memory or take a workspace (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a fixed device-resident array of
+ * sdxl_attn_sublayer_noalloc_max_workspace_bytes() (80 MiB) per GPU, held until the
+ * process ends; calls whose sdxl_attn_sublayer_workspace_bytes exceed it fail with
+ * SDXL_STATUS_INVALID_SHAPE (e.g. [2, 4096, 640] needs 40 MiB, [4, 3840, 640]
+ * 75 MiB). Every call on one GPU shares that array: calls that overlap on one GPU
+ * (concurrent streams, or threads without ordering) race. Allocates nothing, no
+ * host synchronisation; the first call on a device looks up the array's address.
+ * Arguments and results as sdxl_attn_sublayer. */
+size_t sdxl_attn_sublayer_noalloc_max_workspace_bytes(void);
+sdxl_status sdxl_attn_sublayer_noalloc(const sdxl_sublayer_desc* desc, const void* x, const void* ln_gamma,
+                                       const void* ln_beta, const void* w_qkv, const float* w_qkv_scale,
+                                       const void* w_out, const void* b_out, void* y, void* stream);
+
 typedef struct sdxl_cross_sublayer_desc {
     int64_t batch;
     int64_t seq;

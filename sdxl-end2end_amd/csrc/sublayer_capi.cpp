@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <string>
 
 #include "../../include/sdxl_hip/sublayer.h"
@@ -26,9 +27,39 @@ sdxl_status launch_status(hipError_t err, const char* what) {
 
 }  // namespace
 
-extern "C" {
+// Device-resident workspace of sdxl_attn_sublayer_noalloc: one array per GPU,
+// held until the process ends (a .bss symbol of the code object: no file size,
+// no allocation call). Host code never passes `scratch` itself (on the host it
+// names a stand-in, not device memory): the per-device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kScratchBytes = size_t{80} << 20;
+__device__ __attribute__((aligned(256))) unsigned char scratch[kScratchBytes];
 
-}  // extern "C"
+constexpr int kMaxDevices = 64;
+
+// Address of `scratch` on the current device, looked up on the first call on
+// that device; nullptr (and the HIP error text in *err) on failure.
+void* scratch_on_current_device(std::string* err) {
+    static std::mutex mu;
+    static void* ptr[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        *err = e != hipSuccess ? hipGetErrorString(e) : "device index out of range";
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            *err = e != hipSuccess ? hipGetErrorString(e) : "null symbol address";
+            return nullptr;
+        }
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
 
 namespace {
 
@@ -245,6 +276,33 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     od.k = W;
     od.w_dtype = SDXL_DTYPE_F16;
     return sdxl_linear(&od, hidden_ws, w_out, nullptr, b_out, x, y, stream);
+}
+
+size_t sdxl_attn_sublayer_noalloc_max_workspace_bytes(void) { return kScratchBytes; }
+
+sdxl_status sdxl_attn_sublayer_noalloc(const sdxl_sublayer_desc* d, const void* x, const void* ln_gamma,
+                                       const void* ln_beta, const void* w_qkv, const float* w_qkv_scale,
+                                       const void* w_out, const void* b_out, void* y, void* stream) {
+    if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_attn_sublayer_noalloc: null descriptor");
+    if (d->batch < 0 || d->seq < 0 || d->heads <= 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_attn_sublayer_noalloc: invalid shape");
+    int64_t rows = 0;
+    const bool huge = __builtin_mul_overflow(d->batch, d->seq, &rows) || rows > INT32_MAX || d->heads > 65536;
+    const size_t need = huge ? SIZE_MAX : sdxl_attn_sublayer_workspace_bytes(d);
+    if (need > kScratchBytes)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE,
+                             "sdxl_attn_sublayer_noalloc: needs " + std::to_string(need) +
+                                 " workspace bytes (batch * seq * heads * 512), more than the " +
+                                 std::to_string(kScratchBytes) + "-byte device scratch; use sdxl_attn_sublayer");
+    if (d->batch * d->seq == 0) return SDXL_STATUS_OK;
+    std::string err;
+    void* ws = scratch_on_current_device(&err);
+    if (ws == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_LAUNCH_FAILED, "sdxl_attn_sublayer_noalloc: scratch address: " + err);
+    // Every stage writes its part of the workspace before reading it: nothing
+    // needs clearing between calls.
+    return sdxl_attn_sublayer(d, x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, y, ws, kScratchBytes,
+                              stream);
 }
 
 size_t sdxl_cross_attn_sublayer_workspace_bytes(const sdxl_cross_sublayer_desc* d) {

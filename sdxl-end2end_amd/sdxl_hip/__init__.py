@@ -33,6 +33,8 @@ EXPORTED_SYMBOLS = (
     "sdxl_layer_norm_e4m3",
     "sdxl_linear",
     "sdxl_linear_e4m3",
+    "sdxl_attn_sublayer_noalloc",
+    "sdxl_attn_sublayer_noalloc_max_workspace_bytes",
     "sdxl_quantize_e4m3_rows",
     "sdxl_attn_sublayer_workspace_bytes",
     "sdxl_attn_sublayer",
@@ -139,6 +141,10 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sdxl_attn_sublayer.restype = ctypes.c_int
     lib.sdxl_attn_sublayer.argtypes = [ctypes.POINTER(SublayerDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                        ctypes.c_size_t, vp]
+    lib.sdxl_attn_sublayer_noalloc_max_workspace_bytes.restype = ctypes.c_size_t
+    lib.sdxl_attn_sublayer_noalloc_max_workspace_bytes.argtypes = []
+    lib.sdxl_attn_sublayer_noalloc.restype = ctypes.c_int
+    lib.sdxl_attn_sublayer_noalloc.argtypes = [ctypes.POINTER(SublayerDesc), vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.sdxl_cross_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
     lib.sdxl_cross_attn_sublayer_workspace_bytes.argtypes = [ctypes.POINTER(CrossSublayerDesc)]
     lib.sdxl_cross_attn_sublayer.restype = ctypes.c_int
@@ -344,6 +350,19 @@ def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads:
     _check(load().sdxl_attn_sublayer(ctypes.byref(d), _ptr(x), _ptr(ln_gamma), _ptr(ln_beta), _ptr(w_qkv),
                                      _ptr(w_qkv_scale), _ptr(w_out), _ptr(b_out), _ptr(out), _ptr(workspace),
                                      workspace.numel(), _stream(x)))
+    return out
+
+
+def attn_sublayer_noalloc(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads: int, out,
+                          backend: int = AUTO, eps: float = 0.0, fp8_activations: bool = False):
+    """attn_sublayer through the allocation-free entry point (sdxl_attn_sublayer_noalloc): the
+    workspace is the library's fixed per-GPU device array; `out` is caller-provided."""
+    import torch
+    B, S, W = x.shape
+    d = SublayerDesc(batch=B, seq=S, heads=heads, w_qkv_dtype=E4M3 if w_qkv.dtype == torch.uint8 else F16,
+                     attn_backend=backend, ln_eps=eps, qkv_activations=E4M3 if fp8_activations else F16)
+    _check(load().sdxl_attn_sublayer_noalloc(ctypes.byref(d), _ptr(x), _ptr(ln_gamma), _ptr(ln_beta), _ptr(w_qkv),
+                                             _ptr(w_qkv_scale), _ptr(w_out), _ptr(b_out), _ptr(out), _stream(x)))
     return out
 
 
