@@ -377,6 +377,25 @@ def main():
     if args.only == "vae":
         print(json.dumps(bench_vae_attention(torch, sh, args.steps, args.warmup)), flush=True)
         return
+    if args.only in ("qkv", "qkv_fp8"):
+        # profiling aid: the configs[3] QKV projection alone, eager launches (E4M3 weights [1920, 640];
+        # fp16 activations on fp16 MFMA, or E4M3 activations on fp8 MFMA)
+        M, W = 8192, 640
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(7)
+        a = torch.randn(M, W, device="cuda:0", generator=g).half()
+        q8, s8 = sh.quantize_e4m3_rows((torch.randn(3 * W, W, device="cuda:0", generator=g) * 0.02).half())
+        out = torch.empty(M, 3 * W, dtype=torch.float16, device="cuda:0")
+        if args.only == "qkv":
+            fn = lambda: sh.linear(a, q8, w_scale=s8, out=out)
+        else:
+            codes, cs = sh.layer_norm_e4m3(a.view(1, M, W), torch.ones(W, dtype=torch.float16, device="cuda:0"),
+                                           torch.zeros(W, dtype=torch.float16, device="cuda:0"))
+            fn = lambda: sh.linear_e4m3(codes.view(M, W), cs, q8, s8, out=out)
+        for _ in range(args.warmup + args.steps):
+            fn()
+        torch.cuda.synchronize()
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)

@@ -105,11 +105,28 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
     }
 }
 
-// Sum of eight fp32 probabilities as a depth-3 tree. Plain fp32 adds: the
-// packed-dot (v_dot2) alternative shares issue resources with the matrix
-// cores and stalls them.
+// Sum of eight fp32 probabilities as a depth-3 tree.
 __device__ __forceinline__ float sum8(const float* e) {
     return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+}
+
+// Sum of the eight packed fp16/bf16 probabilities in pk[0..3] (fp32
+// accumulation, v_dot2 against ones): the row sum of exactly the values the
+// P.V product uses, four instructions instead of seven adds.
+template <bool IsBf16>
+__device__ __forceinline__ float sum8_packed(const uint32_t* pk) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (IsBf16) {
+            const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[i]), one, s, false);
+        } else {
+            const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+            s = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[i]), one, s, false);
+        }
+    }
+    return s;
 }
 
 // Exchange with lane l ^ 32 (the other half of the wave holds the other keys
@@ -283,55 +300,73 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
 
     // ---- tile transfers: the 16 1-KiB transfers of a K tile plus a V tile are
-    // split over the waves; transfer n covers rows 8*(n%8) .. +7 of K (n < 8) or
-    // V (n >= 8); lane l takes row 8*(n%8) + l/8 and the global chunk
-    // (l%8) ^ swz(row), which lands in its swizzled slot.
-    // Issues the transfers of K tile kt and V tile vt (skipping tiles out of range).
-    // Per-lane offsets are recomputed per tile with 24-bit multiplies (row
-    // strides are below 2^24 bytes, checked on the host) rather than held in
-    // registers; rows past the end of a partial tile re-read the last key.
+    // split over the waves; transfer n covers the 8-row slab n%8 (rows
+    // 8*(n%8) .. +7) of K (n < 8) or V (n >= 8); lane l takes slab row l/8 and
+    // the global chunk (l%8) ^ swz(row), which lands in its swizzled slot.
+    // With row = 8 s + l/8, swz(row) depends only on l and the parity of the
+    // slab s, so a transfer's global offset is a per-lane part for its slab
+    // parity, computed once (24-bit multiplies: row strides are below 2^24
+    // bytes, checked on the host), plus 8 s rows added to the scalar base.
+    auto lane_off = [&](int parity, int64_t stride) __attribute__((always_inline)) -> uint32_t {
+        const int sw = rev3((4 * parity + (lane >> 4)) & 7);
+        return __umul24((uint32_t)(lane >> 3), (uint32_t)stride) + (uint32_t)(((lane & 7) ^ sw) << 4);
+    };
+
+    // Whole and key-split workgroups: wave w issues the four K (w < 2) or V
+    // (w >= 2) slabs of parity w & 1, i.e. slabs 2j + (w & 1), j = 0..3: one
+    // per-lane offset per wave. Issues the transfers of K tile kt and V tile vt
+    // (skipping tiles out of range); rows past the end of a partial last tile
+    // re-read the last key (per-lane clamp, the slow form).
+    const int64_t whole_stride = wave < 2 ? ks_bytes : vs_bytes;
+    const uint32_t whole_off = (!mixed) ? lane_off(wave & 1, whole_stride) : 0u;
     auto issue = [&](int kt, int vt) __attribute__((always_inline)) {
+        const bool is_v = wave >= 2;
+        const int tile = is_v ? vt : kt;
+        if (tile < 0 || tile >= n_tiles) return;
+        const int key0 = tile * kKeyTile;
+        const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
+        if (key0 + kKeyTile <= p.k_seq) {
 #pragma unroll
-        for (int j = 0; j < kLoadsPerWave; ++j) {
-            const int n = wave * kLoadsPerWave + j;
-            const bool is_v = n >= 8;
-            const int tile = is_v ? vt : kt;
-            if (tile < 0 || tile >= n_tiles) continue;
-            const int key0 = tile * kKeyTile;
-            const int64_t stride = is_v ? vs_bytes : ks_bytes;
-            const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * stride;
-            const int row = 8 * (n & 7) + (lane >> 3);
-            const int key = min(row, p.k_seq - 1 - key0);  // clamp rows of a partial tile
-            const uint32_t off = __umul24((uint32_t)key, (uint32_t)stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-            const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
-            lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
+            for (int j = 0; j < kLoadsPerWave; ++j) {
+                const int slab = 2 * j + (wave & 1);
+                const char* slab_base = (is_v ? vbase : kbase) + (int64_t)(key0 + 8 * slab) * whole_stride;
+                lds_dma16(slab_base, whole_off, lds_addr(buf + 8 * slab * kRowBytes));
+            }
+        } else {
+            const char* tile_base = (is_v ? vbase : kbase) + (int64_t)key0 * whole_stride;
+#pragma unroll
+            for (int j = 0; j < kLoadsPerWave; ++j) {
+                const int slab = 2 * j + (wave & 1);
+                const int row = 8 * slab + (lane >> 3);
+                const int key = min(row, p.k_seq - 1 - key0);  // clamp rows of a partial tile
+                const uint32_t off =
+                    __umul24((uint32_t)key, (uint32_t)whole_stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+                lds_dma16(tile_base, off, lds_addr(buf + 8 * slab * kRowBytes));
+            }
         }
     };
 
-    // Key-split stages: transfer n covers 8 rows of one key half (rows 0-31
-    // half 0, 32-63 half 1); stage t holds keys 32t .. +31 of each half.
+    // Key-split stages: slab s covers 8 rows of one key half (slabs 0-3 half
+    // 0, 4-7 half 1); stage t holds keys 32t .. +31 of each half.
     auto issue_split = [&](int kt, int vt) __attribute__((always_inline)) {
+        const bool is_v = wave >= 2;
+        const int tile = is_v ? vt : kt;
+        if (tile < 0 || tile >= n_tiles) return;
+        const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
 #pragma unroll
         for (int j = 0; j < kLoadsPerWave; ++j) {
-            const int n = wave * kLoadsPerWave + j;
-            const bool is_v = n >= 8;
-            const int tile = is_v ? vt : kt;
-            if (tile < 0 || tile >= n_tiles) continue;
-            const int half = (n & 7) >> 2;
-            const int64_t stride = is_v ? vs_bytes : ks_bytes;
-            const char* tile_base = (is_v ? vbase : kbase) + (int64_t)(half * half_keys + 32 * tile) * stride;
-            const int row = 8 * (n & 7) + (lane >> 3);
-            const uint32_t off = __umul24((uint32_t)(row - 32 * half), (uint32_t)stride) +
-                                 (uint32_t)(((lane & 7) ^ swz(row)) << 4);
-            const char* buf = is_v ? vring[tile % kVRing] : kring[tile % kKRing];
-            lds_dma16(tile_base, off, lds_addr(buf + 8 * (n & 7) * kRowBytes));
+            const int slab = 2 * j + (wave & 1), half = slab >> 2;
+            const char* slab_base =
+                (is_v ? vbase : kbase) + (int64_t)(half * half_keys + 32 * tile + 8 * (slab & 3)) * whole_stride;
+            lds_dma16(slab_base, whole_off, lds_addr(buf + 8 * slab * kRowBytes));
         }
     };
 
-    // Mixed workgroups: the 16 transfers of each staged head (its K tile for
-    // m < 8, V tile otherwise, rows 8 (m % 8) .. +7) go to waves m % 12;
-    // k_seq % 64 == 0. The head index is a compile-time loop variable so the
-    // base pointers stay scalars.
+    // Mixed workgroups: the 16 transfers of each staged head go to waves
+    // 0-3 (two K slabs each, 4 (w >> 1) + (w & 1) and that + 2) and waves
+    // 4-11 (V slab w - 4): every wave's slabs have parity w & 1, one per-lane
+    // offset per wave; k_seq % 64 == 0. The head index is a compile-time loop
+    // variable so the base pointers stay scalars.
     const char* set_k0 = (const char*)p.k + ((int64_t)(bh_set[0] / p.heads) * p.k_seq * p.k_row_stride +
                                              (int64_t)(bh_set[0] % p.heads) * kHeadDim) * elem;
     const char* set_k1 = (const char*)p.k + ((int64_t)(bh_set[1] / p.heads) * p.k_seq * p.k_row_stride +
@@ -340,30 +375,23 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                                              (int64_t)(bh_set[0] % p.heads) * kHeadDim) * elem;
     const char* set_v1 = (const char*)p.v + ((int64_t)(bh_set[1] / p.heads) * p.k_seq * p.v_row_stride +
                                              (int64_t)(bh_set[1] % p.heads) * kHeadDim) * elem;
+    const bool mixed_v = wave >= 4;
+    const int64_t mixed_stride = mixed_v ? vs_bytes : ks_bytes;
+    const uint32_t mixed_off = mixed ? lane_off(wave & 1, mixed_stride) : 0u;
     auto issue_mixed = [&](int kt, int vt) __attribute__((always_inline)) {
+        const int tile = mixed_v ? vt : kt;
+        if (tile < 0 || tile >= n_tiles) return;
 #pragma unroll
         for (int sidx = 0; sidx < 2; ++sidx) {
             if (sidx == 1 && nsets == 1) break;
-            const char* kb = sidx ? set_k1 : set_k0;
-            const char* vb = sidx ? set_v1 : set_v0;
+            const char* base = mixed_v ? (sidx ? set_v1 : set_v0) : (sidx ? set_k1 : set_k0);
+            const char* buf = mixed_v ? ring[4 * sidx + kKRing + tile % kVRing] : ring[4 * sidx + tile % kKRing];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int m = wave + kWaves * j;
-                if (m >= 16) continue;
-                const bool is_v = m >= 8;
-                const int tile = is_v ? vt : kt;
-                if (tile < 0 || tile >= n_tiles) continue;
-                const int64_t stride = is_v ? vs_bytes : ks_bytes;
-                const char* tile_base = (is_v ? vb : kb) + (int64_t)(tile * kKeyTile) * stride;
-                // recomputed per tile step (opaque lane copy): held across the
-                // loop, the four offsets would push the loop into spills
-                int ln = lane;
-                asm volatile("" : "+v"(ln));
-                const int row = 8 * (m & 7) + (ln >> 3);
-                const uint32_t off =
-                    __umul24((uint32_t)row, (uint32_t)stride) + (uint32_t)(((ln & 7) ^ swz(row)) << 4);
-                const char* buf = is_v ? ring[4 * sidx + kKRing + tile % kVRing] : ring[4 * sidx + tile % kKRing];
-                lds_dma16(tile_base, off, lds_addr(buf + 8 * (m & 7) * kRowBytes));
+                if (j == 1 && mixed_v) break;
+                const int slab = mixed_v ? wave - 4 : 4 * (wave >> 1) + (wave & 1) + 2 * j;
+                const char* slab_base = base + (int64_t)(tile * kKeyTile + 8 * slab) * mixed_stride;
+                lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
             }
         }
     };
@@ -506,7 +534,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
 #pragma unroll
         for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-        float l_a = sum8(e);
+        float l_a = sum8_packed<IsBf16>(pk);
         if constexpr (kCheck) {
             // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
             // maximum over it and recompute. Rare.
@@ -521,7 +549,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                 for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-                l_a = sum8(e);
+                l_a = sum8_packed<IsBf16>(pk);
             }
         }
         l_run += l_a;
@@ -543,7 +571,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         acc[1] = mfma32<IsBf16>(vop[1], p0, acc[1]);
 #pragma unroll
         for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-        float l_b = sum8(e + 8);
+        float l_b = sum8_packed<IsBf16>(pk + 4);
         if constexpr (kCheck) {
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum)) != 0, 0)) {
                 const float shift = exact_max(s_cur, 8, 16) * ic;
@@ -556,7 +584,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                 for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
 #pragma unroll
                 for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
-                l_b = sum8(e + 8);
+                l_b = sum8_packed<IsBf16>(pk + 4);
             }
         }
         l_run += l_b;
