@@ -33,6 +33,7 @@ PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_attention_c3_traffic.txt")
+CROSS_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "short_keys_attention_cross_traffic.txt")
 
 
 def parse_args():
@@ -276,6 +277,20 @@ def read_traffic():
     return None
 
 
+def read_config_traffic():
+    """{config: HBM bytes per launch} from the committed FETCH_SIZE / WRITE_SIZE summary of the
+    77-key and level-2 shapes."""
+    out = {}
+    try:
+        for line in open(CROSS_TRAFFIC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch["):
+                name = line.split("[", 1)[1].split("]", 1)[0]
+                out[name] = float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return out
+
+
 def cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -442,6 +457,7 @@ def main():
 
     if not args.no_secondary:
         sec = {}
+        measured_traffic = read_config_traffic()
         for name, (b, sq, sk, h, label) in configs.items():
             if name == "c3":
                 continue
@@ -457,6 +473,12 @@ def main():
                          "mfma_frac": round(fl / (k_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4),
                          "hbm_gbs": round(by / (k_ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(by / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+            if name in measured_traffic:
+                # measured HBM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated) over this run's time
+                t = measured_traffic[name]
+                sec[name]["measured_traffic_bytes"] = t
+                sec[name]["measured_hbm_gbs"] = round(t / (k_ms * 1e-3) / 1e9, 1)
+                sec[name]["measured_hbm_frac"] = round(t / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
             del qq, kk, vv
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
         sec["l2_self_sublayer"] = bench_sublayer(torch, sh, B=2, S=1024, H=20)

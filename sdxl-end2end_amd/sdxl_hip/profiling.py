@@ -6,6 +6,10 @@
                                        --copy-fetch DIR --copy-write DIR --copy-mib N
       HBM bytes per launch of NAME from FETCH_SIZE / WRITE_SIZE (KiB per dispatch), each scaled
       by what the same counter reads for a device copy of N MiB (read N MiB, write N MiB).
+  python -m sdxl_hip.profiling report LABEL=DIR_A,DIR_B,KERNEL ...
+      one markdown row per LABEL from two counter passes (PASS_A / PASS_B below) over the
+      dispatches whose name contains KERNEL: MFMA
+      utilisation and per-MFMA instruction and stall ratios (see report_row).
 """
 from __future__ import annotations
 
@@ -59,6 +63,31 @@ def traffic(kernel: str, fetch_dir: str, write_dir: str, copy_fetch: str, copy_w
             "traffic_bytes": f_k * f_scale + w_k * w_scale}
 
 
+PASS_A = ("MfmaUtil", "SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_ACTIVE_INST_VALU", "SQ_WAVE_CYCLES", "SQ_BUSY_CYCLES",
+          "SQ_WAIT_INST_LDS", "SQ_VALU_MFMA_COEXEC_CYCLES")
+PASS_B = ("SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_VALU_CVT", "SQ_INSTS_LDS", "SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT",
+          "SQ_ACTIVE_INST_LDS", "SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "GRBM_GUI_ACTIVE")
+REPORT_HEADER = ("| kernel / workload | MfmaUtil % | MFMA / dispatch | VALU instr / MFMA | exp / MFMA | cvt / MFMA | "
+                 "VALU-active cycles / MFMA | LDS instr / MFMA | LDS bank-conflict % | wave time waiting on s_waitcnt % | "
+                 "wave time waiting to issue % |\n|---|---|---|---|---|---|---|---|---|---|---|")
+
+
+def report_row(label: str, dir_a: str, dir_b: str, kernel: str) -> str:
+    """Per-MFMA ratios of one kernel. Counter semantics used: SQ_INSTS_* count wave instructions
+    (SQ_INSTS_VALU includes the MFMAs); SQ_ACTIVE_INST_VALU, SQ_WAVE_CYCLES and SQ_WAIT_* count in
+    units of 4 shader clocks; MfmaUtil = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE (max over
+    XCDs) * SIMDs) in percent, as rocprofv3 derives it."""
+    a, b = counters(dir_a, kernel), counters(dir_b, kernel)
+    mfma = a["SQ_INSTS_MFMA"]
+    valu = a["SQ_INSTS_VALU"] - mfma
+    waves = a["SQ_WAVE_CYCLES"]
+    conflict = 100.0 * b["SQ_LDS_BANK_CONFLICT"] / max(b["SQ_LDS_IDX_ACTIVE"], 1.0)
+    return (f"| {label} | {a['MfmaUtil']:.1f} | {mfma:.0f} | {valu / mfma:.2f} | "
+            f"{b['SQ_INSTS_VALU_TRANS_F32'] / mfma:.2f} | {b['SQ_INSTS_VALU_CVT'] / mfma:.2f} | "
+            f"{4.0 * a['SQ_ACTIVE_INST_VALU'] / mfma:.1f} | {b['SQ_INSTS_LDS'] / mfma:.2f} | {conflict:.1f} | "
+            f"{100.0 * b['SQ_WAIT_ANY'] / waves:.0f} | {100.0 * b['SQ_WAIT_INST_ANY'] / waves:.0f} |")
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -71,6 +100,8 @@ def main():
     for k in ("kernel", "fetch", "write", "copy_fetch", "copy_write"):
         c.add_argument("--" + k.replace("_", "-"), required=True)
     c.add_argument("--copy-mib", type=float, required=True)
+    r = sub.add_parser("report")
+    r.add_argument("rows", nargs="+", help="LABEL=PASS_A_DIR,PASS_B_DIR,KERNEL_SUBSTRING")
     args = ap.parse_args()
     if args.cmd == "stats":
         for name, (calls, avg, tot) in sorted(kernel_stats(args.dir).items(), key=lambda x: -x[1][2]):
@@ -78,6 +109,12 @@ def main():
     elif args.cmd == "counters":
         for k, v in sorted(counters(args.dir, args.name).items()):
             print(f"{k:32s} {v:18.1f}")
+    elif args.cmd == "report":
+        print(REPORT_HEADER)
+        for row in args.rows:
+            label, dirs = row.split("=", 1)
+            da, db, kernel = dirs.split(",")
+            print(report_row(label, da, db, kernel))
     else:
         t = traffic(args.kernel, args.fetch, args.write, args.copy_fetch, args.copy_write, args.copy_mib)
         for k, v in t.items():
