@@ -8,7 +8,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstddef>
 #include <cstdint>
+#include <limits>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -41,6 +43,19 @@ struct RuntimeOptions {
     // Record an event pair around every Ops call (reference ProfileScope,
     // include/sdxl/cuda/profiler.hpp:32-53); read with Runtime::profile_records().
     bool profile = false;
+    // Bytes of freed device blocks the arena keeps for reuse (reference
+    // RuntimeOptions::arena_cache_limit_bytes, runtime.hpp:80); 0 frees at once.
+    std::size_t arena_cache_limit_bytes = std::numeric_limits<std::size_t>::max();
+};
+
+// Device-memory arena counters (reference MemoryArenaStats, runtime.hpp:114-125).
+struct MemoryArenaStats {
+    std::size_t live_bytes = 0;         // held by live tensors
+    std::size_t cached_bytes = 0;       // freed blocks kept for reuse
+    std::size_t peak_live_bytes = 0;
+    std::size_t driver_allocations = 0; // hipMalloc calls
+    std::size_t cache_hits = 0;         // allocations served from the cache
+    std::size_t graph_held_bytes = 0;   // freed blocks a captured graph may still use
 };
 
 struct ProfileRecord {
@@ -70,6 +85,27 @@ public:
     void end_profile(int id) const;
     // Synchronises and resolves every recorded scope, in order.
     [[nodiscard]] std::vector<ProfileRecord> profile_records() const;
+
+    // Device memory for tensors: a caching arena of exact-size blocks (256-byte
+    // granules). A freed block returns to the cache (up to the option's limit)
+    // and a later allocation of the same size reuses it without a hipMalloc, so
+    // a call sequence repeated after one warm-up pass allocates nothing from
+    // the driver. The deleter of the returned pointer gives the block back.
+    [[nodiscard]] std::shared_ptr<void> allocate_device(std::size_t bytes) const;
+    [[nodiscard]] MemoryArenaStats memory_arena_stats() const noexcept;
+    // Frees every cached block (hipFree); live and graph-held blocks stay.
+    void trim_memory_arena() const;
+
+    // HIP graph capture of Ops calls (reference runtime.hpp:153-157). Between
+    // begin and end, allocations are served from the cache when a block of the
+    // size is there (after a warm-up pass: no driver call inside the capture),
+    // else by hipMalloc; every block allocated in this window is held when its
+    // tensor is freed instead of re-entering the cache, because replays of the
+    // captured graph keep writing it. release_graph_allocations() returns the
+    // held blocks to the cache once the graphs that use them are destroyed.
+    void begin_graph_allocation_capture() const;
+    void end_graph_allocation_capture() const noexcept;
+    void release_graph_allocations() const;
 
 private:
     std::unique_ptr<RuntimeState> state_;

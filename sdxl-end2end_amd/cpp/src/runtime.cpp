@@ -3,7 +3,12 @@
 
 #include "sdxl_hip/attention.h"
 
+#include <algorithm>
+#include <map>
+#include <mutex>
 #include <sstream>
+#include <unordered_map>
+#include <unordered_set>
 
 namespace sdxl::hip {
 
@@ -28,8 +33,79 @@ const char* attention_backend_name(AttentionBackend backend) noexcept {
     return sdxl_attn_backend_name(static_cast<std::int32_t>(backend));
 }
 
+// Caching device-memory arena. Shared by the Runtime and by every block it
+// handed out (the deleters keep it alive), so tensors may outlive the Runtime.
+struct DeviceArena {
+    std::mutex mu;
+    int device = 0;
+    std::size_t cache_limit = 0;
+    std::multimap<std::size_t, void*> free_blocks;           // size -> block
+    std::unordered_map<void*, std::size_t> capture_blocks;   // allocated inside a capture window, live
+    std::vector<std::pair<void*, std::size_t>> graph_held;   // freed, still used by captured graphs
+    bool capturing = false;
+    MemoryArenaStats stats;
+
+    static std::size_t granule(std::size_t bytes) { return (bytes + 255) & ~std::size_t{255}; }
+
+    void* take(std::size_t bytes) {
+        std::lock_guard<std::mutex> lock(mu);
+        void* p = nullptr;
+        auto it = free_blocks.find(bytes);
+        if (it != free_blocks.end()) {
+            p = it->second;
+            free_blocks.erase(it);
+            stats.cached_bytes -= bytes;
+            ++stats.cache_hits;
+        } else {
+            SDXL_HIP_CHECK(hipSetDevice(device));
+            SDXL_HIP_CHECK(hipMalloc(&p, bytes));
+            ++stats.driver_allocations;
+        }
+        stats.live_bytes += bytes;
+        stats.peak_live_bytes = std::max(stats.peak_live_bytes, stats.live_bytes);
+        if (capturing) capture_blocks.emplace(p, bytes);
+        return p;
+    }
+
+    void give_back(void* p, std::size_t bytes) noexcept {
+        std::lock_guard<std::mutex> lock(mu);
+        stats.live_bytes -= bytes;
+        if (capture_blocks.erase(p) != 0) {
+            graph_held.emplace_back(p, bytes);
+            stats.graph_held_bytes += bytes;
+            return;
+        }
+        cache_or_free(p, bytes);
+    }
+
+    void cache_or_free(void* p, std::size_t bytes) noexcept {  // caller holds mu
+        if (stats.cached_bytes + bytes <= cache_limit) {
+            free_blocks.emplace(bytes, p);
+            stats.cached_bytes += bytes;
+        } else {
+            (void)hipSetDevice(device);
+            (void)hipFree(p);
+        }
+    }
+
+    void trim() noexcept {
+        std::lock_guard<std::mutex> lock(mu);
+        (void)hipSetDevice(device);
+        for (auto& [bytes, p] : free_blocks) (void)hipFree(p);
+        free_blocks.clear();
+        stats.cached_bytes = 0;
+    }
+
+    ~DeviceArena() {
+        (void)hipSetDevice(device);
+        for (auto& [bytes, p] : free_blocks) (void)hipFree(p);
+        for (auto& [p, bytes] : graph_held) (void)hipFree(p);
+    }
+};
+
 struct RuntimeState {
     RuntimeOptions options;
+    std::shared_ptr<DeviceArena> arena;
     hipStream_t stream = nullptr;
     struct Scope {
         std::string label;
@@ -46,6 +122,45 @@ Runtime::Runtime(RuntimeOptions options) : state_(std::make_unique<RuntimeState>
     if (options.device < 0 || options.device >= count) throw HipError("HIP device index out of range");
     SDXL_HIP_CHECK(hipSetDevice(options.device));
     SDXL_HIP_CHECK(hipStreamCreateWithFlags(&state_->stream, hipStreamNonBlocking));
+    state_->arena = std::make_shared<DeviceArena>();
+    state_->arena->device = options.device;
+    state_->arena->cache_limit = options.arena_cache_limit_bytes;
+}
+
+std::shared_ptr<void> Runtime::allocate_device(std::size_t bytes) const {
+    if (bytes == 0) return std::shared_ptr<void>();
+    const std::size_t size = DeviceArena::granule(bytes);
+    std::shared_ptr<DeviceArena> arena = state_->arena;
+    void* p = arena->take(size);
+    return std::shared_ptr<void>(p, [arena, size](void* q) { arena->give_back(q, size); });
+}
+
+MemoryArenaStats Runtime::memory_arena_stats() const noexcept {
+    std::lock_guard<std::mutex> lock(state_->arena->mu);
+    return state_->arena->stats;
+}
+
+void Runtime::trim_memory_arena() const { state_->arena->trim(); }
+
+void Runtime::begin_graph_allocation_capture() const {
+    std::lock_guard<std::mutex> lock(state_->arena->mu);
+    if (state_->arena->capturing) throw HipError("HIP graph allocation capture is already active");
+    state_->arena->capturing = true;
+}
+
+void Runtime::end_graph_allocation_capture() const noexcept {
+    std::lock_guard<std::mutex> lock(state_->arena->mu);
+    state_->arena->capturing = false;
+}
+
+void Runtime::release_graph_allocations() const {
+    DeviceArena& a = *state_->arena;
+    std::lock_guard<std::mutex> lock(a.mu);
+    for (auto& [p, bytes] : a.graph_held) {
+        a.stats.graph_held_bytes -= bytes;
+        a.cache_or_free(p, bytes);
+    }
+    a.graph_held.clear();
 }
 
 Runtime::~Runtime() {

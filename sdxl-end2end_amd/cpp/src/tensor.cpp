@@ -111,15 +111,7 @@ Tensor Tensor::allocate(const Runtime& runtime, std::vector<std::size_t> shape, 
     Tensor t;
     t.shape_ = std::move(shape);
     t.type_ = type;
-    const std::size_t bytes = t.bytes();
-    void* ptr = nullptr;
-    if (bytes > 0) {
-        SDXL_HIP_CHECK(hipSetDevice(runtime.device()));
-        SDXL_HIP_CHECK(hipMalloc(&ptr, bytes));
-    }
-    t.data_ = std::shared_ptr<void>(ptr, [](void* p) {
-        if (p != nullptr) (void)hipFree(p);
-    });
+    t.data_ = runtime.allocate_device(t.bytes());  // the runtime's caching arena
     return t;
 }
 

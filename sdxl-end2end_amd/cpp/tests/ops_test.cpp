@@ -200,6 +200,57 @@ void sublayer_cases() {
     std::cout << "sublayer cases passed\n";
 }
 
+// Ops::attention itself (allocating its output) captured in a HIP graph: after
+// one warm-up call the arena serves the output from its cache, so the capture
+// makes no driver allocation; replays with eager work between them reproduce
+// the eager result bit for bit; the block stays held until the graph is gone.
+void graph_capture_cases() {
+    Runtime runtime;
+    Ops ops(runtime);
+    const auto qh = filled({2, 256, 128}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.37F); });
+    const auto kh = filled({2, 300, 128}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.11F); });
+    const auto vh = filled({2, 300, 128}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.05F + 1.0F); });
+    const auto q = Tensor::from_host_f32(runtime, qh);
+    const auto k = Tensor::from_host_f32(runtime, kh);
+    const auto v = Tensor::from_host_f32(runtime, vh);
+    const auto eager = ops.attention(q, k, v, 2).to_host_f32(runtime);  // warm-up: its block returns to the cache
+    const auto before = runtime.memory_arena_stats();
+    require(before.cached_bytes >= q.bytes(), "output block cached after the eager call");
+
+    runtime.begin_graph_allocation_capture();
+    hipGraph_t graph = nullptr;
+    SDXL_HIP_CHECK(hipStreamBeginCapture(runtime.stream(), hipStreamCaptureModeGlobal));
+    Tensor out = ops.attention(q, k, v, 2);
+    SDXL_HIP_CHECK(hipStreamEndCapture(runtime.stream(), &graph));
+    runtime.end_graph_allocation_capture();
+    const auto during = runtime.memory_arena_stats();
+    require(during.driver_allocations == before.driver_allocations, "no hipMalloc inside the capture");
+    require(during.cache_hits == before.cache_hits + 1, "capture served from the arena cache");
+
+    hipGraphExec_t exec = nullptr;
+    SDXL_HIP_CHECK(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    for (int replay = 0; replay < 4; ++replay) {
+        SDXL_HIP_CHECK(hipMemsetAsync(out.data(), 0xFF, out.bytes(), runtime.stream()));  // NaN fill, not captured
+        SDXL_HIP_CHECK(hipGraphLaunch(exec, runtime.stream()));
+        const auto got = out.to_host_f32(runtime);
+        require(got.values.size() == eager.values.size(), "graph output shape");
+        for (std::size_t i = 0; i < got.values.size(); ++i)
+            require(std::memcmp(&got.values[i], &eager.values[i], sizeof(float)) == 0, "graph replay equals eager");
+        (void)ops.attention(k, k, v, 2);  // unrelated eager work between replays
+    }
+    SDXL_HIP_CHECK(hipGraphExecDestroy(exec));
+    SDXL_HIP_CHECK(hipGraphDestroy(graph));
+    const std::size_t held_bytes = out.bytes();
+    out = Tensor();
+    require(runtime.memory_arena_stats().graph_held_bytes >= held_bytes, "captured block held after its tensor died");
+    runtime.release_graph_allocations();
+    const auto released = runtime.memory_arena_stats();
+    require(released.graph_held_bytes == 0, "held blocks released");
+    runtime.trim_memory_arena();
+    require(runtime.memory_arena_stats().cached_bytes == 0, "trim frees the cache");
+    std::cout << "graph capture cases passed\n";
+}
+
 void device_cases() {
     Runtime runtime;
     Ops ops(runtime);
@@ -298,6 +349,7 @@ void device_cases() {
                    "cudnn-sdpa with mask");
     for (float x : cudnn_ops.attention(q2, q2, v2, 1).to_host_f32(cudnn_runtime).values)
         require_close(x, 3.0F, 0.02F, "cudnn-sdpa spelling runs the fused kernel");
+    graph_capture_cases();
     std::cout << "device cases passed\n";
     sublayer_cases();
 }
