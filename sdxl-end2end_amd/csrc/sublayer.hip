@@ -248,7 +248,7 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         const int wr = wn * 64 + 32 * t + col;
-        w_off[t] = wr * kWRowBytes + (kWFp8 ? hf * 8 : 0);
+        w_off[t] = wr * kWRowBytes;
         w_swz[t] = kWFp8 ? (wr >> 2) & 3 : swz(wr);
     }
 
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
             };
             i32x8 wop8[2], aop8[kTMw];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) wop8[t] = op32(wb, w_off[t] - hf * 8, w_swz[t]);
+            for (int t = 0; t < 2; ++t) wop8[t] = op32(wb, w_off[t], w_swz[t]);
 #pragma unroll
             for (int t = 0; t < kTMw; ++t) aop8[t] = op32(ab, a_off[t], a_swz[t]);
 #pragma unroll
@@ -291,37 +291,48 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
                 for (int j = 0; j < 2; ++j) acc[j][i] = mfma32_fp8(wop8[j], aop8[i], acc[j][i]);
             continue;
         }
-        // Operands of K step ks + 1 are read from LDS while step ks's MFMAs run
+        // K order inside a stage: step ks = 2 pp + q (pp = 0, 1; q = 0, 1) has
+        // lane half hf supply the 8 columns 32 pp + 16 hf + 8 q .. +7 of its row
+        // (any order the A and W operands share gives the same sum). Over the two
+        // steps of a pair a lane then needs 16 consecutive columns: one 16-byte
+        // read of E4M3 weight codes per pair (a 64-byte code row holds four such
+        // chunks, swizzled by (row >> 2) & 3, so every 16 lanes of a read hit
+        // all 64 banks), where 8-byte reads per step left half the banks idle.
+        // Operands of step ks + 1 are read from LDS while step ks's MFMAs run
         // (two register sets), so the LDS latency is not exposed at one or two
-        // waves per SIMD. E4M3 weights are read as codes and decoded just
-        // before their step.
+        // waves per SIMD. E4M3 weights are decoded just before their step.
         i16x8 aop[2][kTMw];
-        u32x4 wraw[2][2];  // fp16: the operand; E4M3: codes in the first two dwords
+        u32x4 wraw[2][2];  // fp16: the step's operand; E4M3: the pair's 16 codes
         auto read_ops = [&](int ks, i16x8 (&a)[kTMw], u32x4 (&w)[2]) __attribute__((always_inline)) {
+            const int pp = ks >> 1, q = ks & 1;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if constexpr (kWFp8) {
-                    const u32x2 raw = *(const lds_u32x2*)(wb + w_off[t] + ((ks ^ w_swz[t]) << 4));
-                    w[t] = u32x4{raw[0], raw[1], 0u, 0u};
+                    if (q == 0) w[t] = *(const lds_u32x4*)(wb + w_off[t] + (((2 * pp + hf) ^ w_swz[t]) << 4));
                 } else {
-                    w[t] = __builtin_bit_cast(u32x4, *(const lds_i16x8*)(wb + w_off[t] + (((2 * ks + hf) ^ w_swz[t]) << 4)));
+                    w[t] = __builtin_bit_cast(
+                        u32x4, *(const lds_i16x8*)(wb + w_off[t] + (((4 * pp + 2 * hf + q) ^ w_swz[t]) << 4)));
                 }
             }
 #pragma unroll
             for (int t = 0; t < kTMw; ++t)
-                a[t] = *(const lds_i16x8*)(ab + a_off[t] + (((2 * ks + hf) ^ a_swz[t]) << 4));
+                a[t] = *(const lds_i16x8*)(ab + a_off[t] + (((4 * pp + 2 * hf + q) ^ a_swz[t]) << 4));
         };
         read_ops(0, aop[0], wraw[0]);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int cur = ks & 1;
-            if (ks < 3) read_ops(ks + 1, aop[cur ^ 1], wraw[cur ^ 1]);
+            // E4M3: the pair's codes are read at its first step, into the set
+            // of that step's parity
+            const int wset = kWFp8 ? ((ks >> 1) & 1) : cur;
+            if (ks < 3) read_ops(ks + 1, aop[cur ^ 1], wraw[kWFp8 ? (((ks + 1) >> 1) & 1) : cur ^ 1]);
             __builtin_amdgcn_sched_barrier(0);  // keep the next step's reads ahead of this step's MFMAs
             i16x8 wop[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 if constexpr (kWFp8) {
-                    const uint2 lo = e4m3x4_to_f16(wraw[cur][t][0]), hi = e4m3x4_to_f16(wraw[cur][t][1]);
+                    const int d = 2 * (ks & 1);  // dwords 0-1: step 2pp, dwords 2-3: step 2pp + 1
+                    const uint2 lo = e4m3x4_to_f16(wraw[wset][t][d]), hi = e4m3x4_to_f16(wraw[wset][t][d + 1]);
                     wop[t] = __builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
                 } else {
                     wop[t] = __builtin_bit_cast(i16x8, wraw[cur][t]);
