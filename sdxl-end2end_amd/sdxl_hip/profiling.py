@@ -1,6 +1,7 @@
 """Summaries of rocprofv3 output for the attention kernels (CSV output format).
 
-  python -m sdxl_hip.profiling stats <dir>            kernel-trace stats (per-kernel avg duration)
+  python -m sdxl_hip.profiling stats <dir> [--last N] kernel-trace stats (per-kernel avg duration;
+                                                      --last N: over each kernel's last N dispatches)
   python -m sdxl_hip.profiling counters <dir> [name]  mean PMC counter value per dispatch of a kernel
   python -m sdxl_hip.profiling traffic --kernel NAME --fetch DIR --write DIR
                                        --copy-fetch DIR --copy-write DIR --copy-mib N
@@ -26,9 +27,18 @@ def _rows(root: str, suffix: str):
             yield from csv.DictReader(fh)
 
 
-def kernel_stats(root: str):
-    """{kernel: (calls, avg_ns, total_ns)} from *kernel_stats.csv (or *kernel_trace.csv)."""
+def kernel_stats(root: str, last: int = 0):
+    """{kernel: (calls, avg_ns, total_ns)} from *kernel_stats.csv (or *kernel_trace.csv); with
+    last > 0, from the trace over each kernel's last `last` dispatches (in start order)."""
     out = {}
+    if last > 0:
+        acc = defaultdict(list)
+        for r in _rows(root, "kernel_trace.csv"):
+            acc[r["Kernel_Name"]].append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+        for k, v in acc.items():
+            d = [e - s for s, e in sorted(v)[-last:]]
+            out[k] = (len(d), sum(d) / len(d), float(sum(d)))
+        return out
     for r in _rows(root, "kernel_stats.csv"):
         out[r["Name"]] = (int(r["Calls"]), float(r["AverageNs"]), float(r["TotalDurationNs"]))
     if not out:
@@ -93,6 +103,7 @@ def main():
     sub = ap.add_subparsers(dest="cmd", required=True)
     a = sub.add_parser("stats")
     a.add_argument("dir")
+    a.add_argument("--last", type=int, default=0)
     b = sub.add_parser("counters")
     b.add_argument("dir")
     b.add_argument("name", nargs="?", default="")
@@ -104,7 +115,7 @@ def main():
     r.add_argument("rows", nargs="+", help="LABEL=PASS_A_DIR,PASS_B_DIR,KERNEL_SUBSTRING")
     args = ap.parse_args()
     if args.cmd == "stats":
-        for name, (calls, avg, tot) in sorted(kernel_stats(args.dir).items(), key=lambda x: -x[1][2]):
+        for name, (calls, avg, tot) in sorted(kernel_stats(args.dir, args.last).items(), key=lambda x: -x[1][2]):
             print(f"{avg / 1e3:10.2f} us avg  {calls:6d} calls  {tot / 1e6:9.3f} ms total  {name[:110]}")
     elif args.cmd == "counters":
         for k, v in sorted(counters(args.dir, args.name).items()):
