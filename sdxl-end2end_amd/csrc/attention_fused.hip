@@ -448,17 +448,18 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         }
     };
 
-    // Exact-maximum pass over raw scores sc[i0, i1) (c * sc relative to
-    // m_run): moves the anchor where needed (anchored rows move up only,
-    // unanchored rows take any finite maximum), rescales O and l and returns
-    // the shift (log2 units) every exp2 argument formed against the old anchor
-    // must subtract; raw scores subtract shift / c (times ic = 1 / c).
+    // Exact-maximum pass over the exp2 arguments sc[i0, i1) (scaled scores,
+    // relative to m_run): moves the anchor where needed (anchored rows move up
+    // only, unanchored rows take any finite maximum), rescales O and l and
+    // returns the shift (log2 units) every exp2 argument formed against the
+    // old anchor must subtract; raw (unscaled) scores subtract shift / c
+    // (times ic = 1 / c).
     auto exact_max = [&](const f32x16& sc, int i0, int i1) __attribute__((always_inline)) -> float {
         float mx = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             if (i >= i0 && i < i1) mx = fmaxf(mx, sc[i]);
-        mx = xhalf_max(mx) * c;  // c > 0
+        mx = xhalf_max(mx);
         const bool move = anchored ? mx > 0.0f : mx > -__builtin_inff();
         const float shift = move ? mx : 0.0f;
         const float alpha = anchored ? __builtin_amdgcn_exp2f(-shift) : 0.0f;
@@ -479,7 +480,8 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         return shift;
     };
 
-    // One pipelined group step (32 keys of tile t, group g; scores in s_cur).
+    // One pipelined group step (32 keys of tile t, group g; s_cur holds its
+    // exp2 arguments c * S - m, scaled in place during the previous step).
     // Overlapped inside the wave: the next group's QK^T chain (K operands in
     // kop, prefetched one step earlier) runs on the matrix core while this
     // group's exponentials run on the VALU; P.V of each 16-key half follows as
@@ -508,7 +510,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             }
         }
         if constexpr (kMasked || kExact) {
-            const float shift = exact_max(s_cur, 0, 16) * ic;
+            const float shift = exact_max(s_cur, 0, 16);
 #pragma unroll
             for (int i = 0; i < 16; ++i) s_cur[i] -= shift;
         }
@@ -519,16 +521,17 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // Eight slots, each one MFMA followed by about its duration (32 cycles)
         // of VALU work that does not depend on it, pinned with scheduling
         // barriers: the wave keeps issuing while the matrix core runs, and the
-        // dependent QK^T chain always has a slot between its links.
+        // dependent QK^T chain always has a slot between its links. The next
+        // group's raw scores are scaled in slots 6-8, after its chain is done.
         // 1: QK1 | exp 0-3
         s_next = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+        for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
         // 2: QK2 | exp 4-7
         s_next = mfma32<IsBf16>(kop[1], qop[1], s_next);
 #pragma unroll
-        for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+        for (int i = 4; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
         // 3: QK3 | pack + row sum of half 0, overflow check
         s_next = mfma32<IsBf16>(kop[2], qop[2], s_next);
@@ -539,14 +542,15 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             // Half 0 rose far above the anchor (sum > 2^14, or inf/NaN): exact
             // maximum over it and recompute. Rare.
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_a <= kOverflowSum)) != 0, 0)) {
-                const float shift = exact_max(s_cur, 0, 8) * ic;
+                const float shift = exact_max(s_cur, 0, 8);
+                const float raw_shift = shift * ic;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     s_cur[i] -= shift;
-                    s_next[i] -= shift;  // partial QK^T sum seeded with the old anchor
+                    s_next[i] -= raw_shift;  // partial QK^T sum seeded with the old anchor
                 }
 #pragma unroll
-                for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+                for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
                 l_a = sum8_packed<IsBf16>(pk);
@@ -557,14 +561,14 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         // 4: QK4 | exp 8-11
         s_next = mfma32<IsBf16>(kop[3], qop[3], s_next);
 #pragma unroll
-        for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+        for (int i = 8; i < 12; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         __builtin_amdgcn_sched_barrier(0);
         // 5: PV half 0, d 0-31 | exp 12-15; K operands of the group after next
         // (unconditional: stale data past the last tile is never used)
         const i16x8 p0 = __builtin_bit_cast(i16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
         acc[0] = mfma32<IsBf16>(vop[0], p0, acc[0]);
 #pragma unroll
-        for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+        for (int i = 12; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
         if constexpr (kPrefetchK) load_k(kn2, g2, kop);
         __builtin_amdgcn_sched_barrier(0);
         // 6: PV half 0, d 32-63 | pack + row sum of half 1, overflow check
@@ -574,14 +578,15 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         float l_b = sum8_packed<IsBf16>(pk + 4);
         if constexpr (kCheck) {
             if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(l_b <= kOverflowSum)) != 0, 0)) {
-                const float shift = exact_max(s_cur, 8, 16) * ic;
+                const float shift = exact_max(s_cur, 8, 16);
+                const float raw_shift = shift * ic;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     s_cur[i] -= shift;
-                    s_next[i] -= shift;
+                    s_next[i] -= raw_shift;
                 }
 #pragma unroll
-                for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i] * c);
+                for (int i = 8; i < 16; ++i) e[i] = __builtin_amdgcn_exp2f(s_cur[i]);
 #pragma unroll
                 for (int i = 4; i < 8; ++i) pk[i] = pack2<IsBf16>(e[2 * i], e[2 * i + 1]);
                 l_b = sum8_packed<IsBf16>(pk + 4);
@@ -590,10 +595,16 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         l_run += l_b;
         load_v(vb, g, 1, vop);
         __builtin_amdgcn_sched_barrier(0);
-        // 7, 8: PV half 1
+        // 7: PV half 1, d 0-31 | scale the next group's scores 0-7
         const i16x8 p1 = __builtin_bit_cast(i16x8, u32x4{pk[4], pk[5], pk[6], pk[7]});
         acc[0] = mfma32<IsBf16>(vop[0], p1, acc[0]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s_next[i] *= c;
+        __builtin_amdgcn_sched_barrier(0);
+        // 8: PV half 1, d 32-63 | scale the next group's scores 8-15
         acc[1] = mfma32<IsBf16>(vop[1], p1, acc[1]);
+#pragma unroll
+        for (int i = 8; i < 16; ++i) s_next[i] *= c;
         (void)have_next;
     };
 
@@ -616,6 +627,8 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
         for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[i] *= c;  // exp2 arguments of the first group
         auto stage = [&]<bool kFirst, bool kOdd>(int t) __attribute__((always_inline)) {
             wait_vmem_all();  // this lane's transfers of K(t+1), V(t) landed
             __syncthreads();  // ... and every lane's; stage t-1 fully consumed
@@ -646,6 +659,8 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
         for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[i] *= c;  // exp2 arguments of the first group
         if (!half_wave) load_k(kring[0], 1, kop);
         // Whole and half waves run separate loops (same barrier sequence), so
         // each keeps its own register allocation.
@@ -695,6 +710,8 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
 #pragma unroll
         for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[i] *= c;  // exp2 arguments of the first group
         load_k(kring[0], 1, kop);
     }
     // kOdd: parity of t, so that every ring slot below is a compile-time
