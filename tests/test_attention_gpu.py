@@ -363,6 +363,9 @@ def test_hip_graph_capture_replays():
     (1, 256, 512, 2),     # 4 units -> 8 key-split workgroups
     (2, 384, 1088, 3),    # 18 units, Sk not a multiple of 128
     (1, 3584, 512, 60),   # 1680 units: two full rounds of whole workgroups, then a mixed round
+    (1, 1024, 192, 8),    # 64 units -> 128 key-split workgroups, 3 key tiles
+    (1, 1024, 1088, 24),  # 192 units -> 384 key-split workgroups, 17 key tiles
+    (2, 1024, 1024, 20),  # 320 units (the level-2 self-attention) -> 640 key-split workgroups
 ])
 def test_key_split_workgroups(B, Sq, Sk, H):
     qb, kb, vb = seeded(880 + Sq, B, Sq, H * 64), seeded(881 + Sk, B, Sk, H * 64), seeded(882, B, Sk, H * 64)
