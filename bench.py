@@ -263,6 +263,11 @@ def bench_cross_sublayer(torch, sh, steps=50, warmup=5):
     ms = time_fn(torch, lambda: sh.cross_attn_sublayer(x, gamma, beta, w_q, None, kv, w_out, b_out, H, out=y,
                                                        workspace=ws), steps, warmup)
     out["fused_call_us"] = round(ms * 1e3, 2)
+    # the same call with an explicit backend: the four-launch composition (LayerNorm, q projection,
+    # attention, out-projection) instead of the q projection and attention in one launch
+    ms = time_fn(torch, lambda: sh.cross_attn_sublayer(x, gamma, beta, w_q, None, kv, w_out, b_out, H, out=y,
+                                                       workspace=ws, backend=sh.FLASH_SM80), steps, warmup)
+    out["composed_call_us"] = round(ms * 1e3, 2)
     return out
 
 

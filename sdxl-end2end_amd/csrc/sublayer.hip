@@ -47,6 +47,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 struct u32x4x2 {
     u32x4 lo, hi;
 };
@@ -122,7 +124,11 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 // (64-byte rows, chunk swizzle (row >> 2) & 3) and are decoded when the
 // operand is read; fp16 weights use the A-operand layout. kAFp8 (with kWFp8):
 // E4M3 activations in 64-byte rows, fp8 MFMA.
-template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2>
+// kKvG > 0: the query projection of the cross-attention (64 x 128 tiles, so
+// each wave's 32 x 64 block is one 32-row query block of one head) fused
+// with the attention over kKvG 32-key groups of context (kKvHalf: the last
+// group holds at most 16 keys); see the epilogue.
+template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2, int kKvG = 0, bool kKvHalf = false>
 __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p) {
     static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
     constexpr int kBMt = 64 * kTM;
@@ -144,6 +150,10 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
     constexpr int kStageBytes = kATileBytes + kWTileBytes;
     constexpr int kSmemStages = kRing * kStageBytes >= kWaves * 32 * 256 ? kRing : (kWaves * 32 * 256 + kStageBytes - 1) / kStageBytes;
     __shared__ __attribute__((aligned(16))) char smem[kSmemStages][kStageBytes];
+    // V rows of the tile's two heads (cross-attention form), swizzled 128-byte
+    // rows: every row a key group reads (kKvHalf: 16 of the last group's 32)
+    constexpr int kVRows = kKvG > 0 ? 32 * (kKvG - 1) + (kKvHalf ? 16 : 32) : 1;
+    __shared__ __attribute__((aligned(16))) char vbuf[2 * kVRows * kRowBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -252,6 +262,33 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
         w_swz[t] = kWFp8 ? (wr >> 2) & 3 : swz(wr);
     }
 
+    // Cross-attention form: the wave's K operands go to registers and both
+    // heads' V rows to LDS now, ahead of the stages (older loads: the stage
+    // waits cover them), so their latency hides under the main loop.
+    i16x8 kreg[kKvG > 0 ? kKvG : 1][4];
+    if constexpr (kKvG > 0) {
+        const int64_t ldkv_b = p.ldkv * 2;
+        const char* kvb = (const char*)p.kv + (int64_t)(m0 / p.seq) * p.ctx_len * ldkv_b;
+        const char* kh = kvb + (int64_t)(n0 + wn * 64) * 2;
+#pragma unroll
+        for (int g = 0; g < kKvG; ++g) {
+            const int key = min(32 * g + col, p.ctx_len - 1);  // rows past ctx_len: never visible
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) kreg[g][ks] = *(const i16x8*)(kh + key * ldkv_b + (2 * ks + hf) * 16);
+        }
+        constexpr int kVXfers = 2 * kVRows / 8 / kWaves;  // 1-KiB transfers per wave
+        static_assert(kVXfers * kWaves * 8 == 2 * kVRows, "V transfers");
+        const char* vb0 = kvb + (int64_t)(p.n + n0) * 2;
+#pragma unroll
+        for (int j = 0; j < kVXfers; ++j) {
+            const int t = wave * kVXfers + j;
+            const int hl = t / (kVRows / 8), r8 = t % (kVRows / 8);
+            const int row = 8 * r8 + (lane >> 3);
+            const uint32_t off =
+                (uint32_t)(min(row, p.ctx_len - 1) * ldkv_b) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            lds_dma16(vb0 + hl * 128, off, lds_addr(vbuf + (hl * kVRows + 8 * r8) * kRowBytes));
+        }
+    }
 #pragma unroll
     for (int st = 0; st < kRing - 1; ++st)
         if (st < n_stages) issue_stage(st);
@@ -359,6 +396,141 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
     char* eb = &smem[0][0] + wave * (32 * 256);
     static_assert(sizeof(smem) >= kWaves * 32 * 256, "epilogue staging fits in the stage buffers");
     __syncthreads();  // every wave is done with the stage buffers
+    if constexpr (kKvG > 0) {
+        // ---- cross-attention epilogue. (1) The wave's fp16 query block,
+        // computed exactly as the plain epilogue would store it (same parking,
+        // scale and rounding), goes to LDS as 32 swizzled 128-byte rows.
+        static_assert(kTMw == 1 && kWM == 2, "one 32 x 64 query block per wave");
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = 8 * j + 2 * u + hf;
+                *(lds_f32x4*)(eb + col * 256 + ((c ^ (col & 15)) << 4)) =
+                    f32x4{acc[j][0][4 * u], acc[j][0][4 * u + 1], acc[j][0][4 * u + 2], acc[j][0][4 * u + 3]};
+            }
+        const int rq0 = m0 + wm * 32 + (lane >> 4);
+        uint2 qv[8];
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int r = 4 * it + (lane >> 4);
+            const float rs = kAFp8 ? p.a_scale[rq0 + 4 * it] : 1.0f;
+            const f32x4 a = *(const lds_f32x4*)(eb + r * 256 + ((ec ^ (r & 15)) << 4));
+            // fp32 value first, then fp16 (as the plain epilogue and the
+            // reference round): the empty asm keeps the compiler from
+            // rounding the fma straight to fp16 in one step
+            f32x4 v = {a[0] * rs * e_scale.x + e_bias.x, a[1] * rs * e_scale.y + e_bias.y,
+                       a[2] * rs * e_scale.z + e_bias.z, a[3] * rs * e_scale.w + e_bias.w};
+            asm volatile("" : "+v"(v));
+            const f16x4 h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+            qv[it] = __builtin_bit_cast(uint2, h);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // parked values read before the rows are reused
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            const int r = 4 * it + (lane >> 4);
+            *(lds_u32x2*)(eb + r * kRowBytes + (((ec >> 1) ^ swz(r)) << 4) + 8 * (ec & 1)) = u32x2{qv[it].x, qv[it].y};
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // (2) One-pass exact softmax over the ctx_len keys (the short-key
+        // attention's block step): S^T = K Q^T with K from registers, one
+        // maximum, exp2, one sum, O^T = V^T P^T with V^T by transposing reads.
+        const int k_swz = swz(col);
+        i16x8 qop[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) qop[ks] = *(const lds_i16x8*)(eb + col * kRowBytes + (((2 * ks + hf) ^ k_swz) << 4));
+        f32x16 seed_last;
+        {
+            const int lim = p.ctx_len - 32 * (kKvG - 1) - 4 * hf;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) seed_last[i] = 8 * (i >> 2) + (i & 3) < lim ? 0.0f : -__builtin_inff();
+        }
+        f32x16 s[kKvG];
+#pragma unroll
+        for (int g = 0; g < kKvG; ++g) {
+            f32x16 z = {};
+            s[g] = mfma32(kreg[g][0], qop[0], g == kKvG - 1 ? seed_last : z);
+        }
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks)
+#pragma unroll
+            for (int g = 0; g < kKvG; ++g) s[g] = mfma32(kreg[g][ks], qop[ks], s[g]);
+        constexpr int kLastN = kKvHalf ? 8 : 16;
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int g = 0; g < kKvG; ++g)
+#pragma unroll
+            for (int i = 0; i < (g == kKvG - 1 ? kLastN : 16); ++i) mx = fmaxf(mx, s[g][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float c = p.scale_log2;
+        const float neg_cm = -c * mx;  // ctx_len > 0: every row has a visible key
+        const int g16 = lane & 15;
+        const int tr_key = 4 * hf + (g16 >> 2), tr_qd = g16 & 3;
+        int v_off[2][2];
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+            const int chunk = 4 * dt + 2 * ((lane >> 4) & 1) + (tr_qd >> 1);
+#pragma unroll
+            for (int hi = 0; hi < 2; ++hi)
+                v_off[dt][hi] = (tr_key + 8 * hi) * kRowBytes + ((chunk ^ swz(tr_key + 8 * hi)) << 4) + ((tr_qd & 1) << 3);
+        }
+        const char* vh = vbuf + wn * (kVRows * kRowBytes);
+        f32x16 out[2] = {};
+        float l = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kKvG; ++g) {
+            const int n_ss = (kKvHalf && g == kKvG - 1) ? 1 : 2;
+            float e[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) e[i] = i < 8 * n_ss ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[g][i], c, neg_cm)) : 0.0f;
+            float ls = 0.0f;
+#pragma unroll
+            for (int h8 = 0; h8 < 2; ++h8)
+                if (h8 < n_ss)
+                    ls += ((e[8 * h8] + e[8 * h8 + 1]) + (e[8 * h8 + 2] + e[8 * h8 + 3])) +
+                          ((e[8 * h8 + 4] + e[8 * h8 + 5]) + (e[8 * h8 + 6] + e[8 * h8 + 7]));
+            l += ls;
+#pragma unroll
+            for (int ss = 0; ss < n_ss; ++ss) {
+                u32x4 pw;
+#pragma unroll
+                for (int w2 = 0; w2 < 4; ++w2) {
+                    const f16x2 pr = {(_Float16)e[8 * ss + 2 * w2], (_Float16)e[8 * ss + 2 * w2 + 1]};
+                    pw[w2] = __builtin_bit_cast(uint32_t, pr);
+                }
+                const i16x8 pop = __builtin_bit_cast(i16x8, pw);
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    const char* base = vh + (32 * g + 16 * ss) * kRowBytes;
+                    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][0]));
+                    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt][1]));
+                    out[dt] = mfma32(i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pop, out[dt]);
+                }
+            }
+        }
+        const float l_tot = l + __shfl_xor(l, 32, 64);
+        const float inv = 1.0f / l_tot;
+        // (3) Output rows through the same buffer (the query rows are in
+        // registers), then whole 128-byte row segments per 8 lanes.
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const f16x2 w0 = {(_Float16)(out[dt][4 * u] * inv), (_Float16)(out[dt][4 * u + 1] * inv)};
+                const f16x2 w1 = {(_Float16)(out[dt][4 * u + 2] * inv), (_Float16)(out[dt][4 * u + 3] * inv)};
+                *(lds_u32x2*)(eb + col * kRowBytes + (((4 * dt + u) ^ k_swz) << 4) + 8 * hf) =
+                    u32x2{__builtin_bit_cast(uint32_t, w0), __builtin_bit_cast(uint32_t, w1)};
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        _Float16* ob = (_Float16*)p.c + (int64_t)(m0 + wm * 32) * p.ldc + n0 + wn * 64 + 8 * (lane & 7);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            const u32x4 w = *(const lds_u32x4*)(eb + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+            store_out<kNt>(w, (u32x4*)(ob + (int64_t)row * p.ldc));
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < kTMw; ++i) {
         const int rm0 = m0 + wm * 32 * kTMw + 32 * i + (lane >> 4);  // row of iteration it: rm0 + 4 it
@@ -716,6 +888,45 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
         else SDXL_LIN(false, false, 2, 2);
     }
 #undef SDXL_LIN
+    return hipGetLastError();
+}
+
+// Workgroups of the fused kernel resident per CU (LDS: 52 KiB with E4M3
+// weights and fp16 activations, 56 or 68 KiB otherwise).
+int q_cross_attention_per_cu(bool w_fp8, bool a_fp8) { return w_fp8 && !a_fp8 ? 3 : 2; }
+
+bool q_cross_attention_supported(const LinearParams& p, bool w_fp8, int compute_units) {
+    // one round: a second round of a few workgroups costs more than the
+    // saved launch and query round trip
+    const int64_t tasks = p.m > 0 ? (int64_t)(p.m / 64) * (p.n / 128) : 0;
+    if (compute_units <= 0 || tasks > (int64_t)q_cross_attention_per_cu(w_fp8, p.a_scale != nullptr) * compute_units)
+        return false;
+    return p.m > 0 && p.seq > 0 && p.seq % 64 == 0 && p.m % p.seq == 0 && p.n % 128 == 0 && p.k % kBK == 0 &&
+           p.ctx_len >= 65 && p.ctx_len <= 80 && p.kv != nullptr && p.bias == nullptr && p.residual == nullptr &&
+           p.ldkv >= 2 * (int64_t)p.n && p.ldkv % 8 == 0 && ((uintptr_t)p.kv & 15) == 0 && p.ldc % 8 == 0 &&
+           ((uintptr_t)p.c & 15) == 0 && (int64_t)(p.m / 64) * (p.n / 128) <= 0x7FFFFFFF;
+}
+
+hipError_t launch_q_cross_attention(const LinearParams& params_in, bool w_fp8, int compute_units, hipStream_t stream) {
+    LinearParams p = params_in;
+    const bool a_fp8 = p.a_scale != nullptr;
+    if (!q_cross_attention_supported(p, w_fp8, compute_units) || (a_fp8 && !w_fp8)) return hipErrorInvalidValue;
+    // 64 x 128 tiles in row-major task order; 65-80 keys are three 32-key
+    // groups, the last holding at most 16.
+    p.m_blocks = p.m / 64;
+    p.n_blocks = p.n / kBN;
+    p.group_m = 1;
+    const dim3 grid((unsigned)((int64_t)p.m_blocks * p.n_blocks)), block(256);
+    const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;
+#define SDXL_QX(WF, AF)                                                                                              \
+    do {                                                                                                             \
+        if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, 1, 2, 2, true, 2, 3, true>), grid, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((linear_kernel<WF, AF, 1, 2, 2, false, 2, 3, true>), grid, block, 0, stream, p);    \
+    } while (0)
+    if (a_fp8) SDXL_QX(true, true);
+    else if (w_fp8) SDXL_QX(true, false);
+    else SDXL_QX(false, false);
+#undef SDXL_QX
     return hipGetLastError();
 }
 

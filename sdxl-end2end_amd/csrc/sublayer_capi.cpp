@@ -5,6 +5,7 @@
 // with the context K/V projected once per request (src/cuda/unet.cpp:120-131).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -347,15 +348,50 @@ sdxl_status sdxl_cross_attn_sublayer(const sdxl_cross_sublayer_desc* d, const vo
     qd.k = W;
     qd.w_dtype = d->w_q_dtype;
     sdxl_status st;
-    if (act_fp8) {
-        st = sdxl_layer_norm_e4m3(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, codes, 0, code_scale, stream);
-        if (st != SDXL_STATUS_OK) return st;
-        st = sdxl_linear_e4m3(&qd, codes, code_scale, w_q, w_q_scale, nullptr, nullptr, q, stream);
-    } else {
-        st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
-        if (st != SDXL_STATUS_OK) return st;
-        st = sdxl_linear(&qd, hidden_ws, w_q, w_q_scale, nullptr, nullptr, q, stream);
+    if (act_fp8) st = sdxl_layer_norm_e4m3(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, codes, 0, code_scale, stream);
+    else st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+    if (st != SDXL_STATUS_OK) return st;
+
+    // Query projection and attention in one launch where the shapes allow it
+    // (the 77-token context, sequences in 64-row tiles, 128-column head
+    // pairs, a grid resident at once) and the backend is left to the
+    // library: each wave attends with
+    // the 32 x 64 query block it has just projected, which never leaves the
+    // CU. Its output (the attention output) goes to the second workspace
+    // region while other workgroups still read the LayerNorm output.
+    const bool w_fp8 = d->w_q_dtype == SDXL_DTYPE_E4M3;
+    if (d->attn_backend == SDXL_ATTN_AUTO && (!w_fp8 || w_q_scale != nullptr) && w_q != nullptr &&
+        aligned(w_q, 16) && (W * (w_fp8 ? 1 : 2)) % 16 == 0 && (w_q_scale == nullptr || aligned(w_q_scale, 16))) {
+        sdxl_hip::LinearParams p{};
+        p.a = act_fp8 ? static_cast<const void*>(codes) : hidden_ws;
+        p.a_scale = act_fp8 ? code_scale : nullptr;
+        p.w = w_q;
+        p.w_scale = w_q_scale;
+        p.c = q;
+        p.lda = p.ldw = p.ldc = p.ldr = W;
+        p.m = (int32_t)M;
+        p.n = p.k = (int32_t)W;
+        p.kv = kv;
+        p.ldkv = ldkv;
+        p.ctx_len = (int32_t)d->ctx_len;
+        p.seq = (int32_t)d->seq;
+        p.scale_log2 = (1.0f / std::sqrt(64.0f)) * 1.4426950408889634f;
+        if (M <= INT32_MAX && W <= INT32_MAX && sdxl_hip::q_cross_attention_supported(p, w_fp8, compute_units())) {
+            st = launch_status(
+                sdxl_hip::launch_q_cross_attention(p, w_fp8, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                "sdxl_cross_attn_sublayer");
+            if (st != SDXL_STATUS_OK) return st;
+            sdxl_linear_desc od{};
+            od.m = M;
+            od.n = W;
+            od.k = W;
+            od.w_dtype = SDXL_DTYPE_F16;
+            return sdxl_linear(&od, q, w_out, nullptr, b_out, x, y, stream);
+        }
     }
+
+    if (act_fp8) st = sdxl_linear_e4m3(&qd, codes, code_scale, w_q, w_q_scale, nullptr, nullptr, q, stream);
+    else st = sdxl_linear(&qd, hidden_ws, w_q, w_q_scale, nullptr, nullptr, q, stream);
     if (st != SDXL_STATUS_OK) return st;
 
     sdxl_attn_desc ad{};

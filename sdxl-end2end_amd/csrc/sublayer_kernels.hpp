@@ -24,9 +24,22 @@ struct LinearParams {
     int32_t m, n, k;
     int32_t m_blocks, n_blocks;  // filled by the launcher
     int32_t group_m;             // filled by the launcher: m blocks per task group
+    // Query projection fused with the 77-token cross-attention
+    // (launch_q_cross_attention only): kv [batch, ctx_len, ldkv] holds K in
+    // columns 0 .. n-1 and V in n .. 2n-1; c receives the attention output.
+    const void* kv;
+    int64_t ldkv;
+    int32_t ctx_len, seq;
+    float scale_log2;
 };
 // compute_units: CUs of the device (tile-size choice).
 hipError_t launch_linear(const LinearParams& params, bool w_fp8, int compute_units, hipStream_t stream);
+// q = a w^T (64 x 128 tiles, one 32-row block of one head per wave), then
+// softmax(q k^T * scale) v per head, written to c. Requires seq % 64 == 0,
+// n % 128 == 0 (heads of 64), 65 <= ctx_len <= 80, k % 64 == 0, no bias or
+// residual, and a grid that is resident at once on compute_units CUs.
+bool q_cross_attention_supported(const LinearParams& params, bool w_fp8, int compute_units);
+hipError_t launch_q_cross_attention(const LinearParams& params, bool w_fp8, int compute_units, hipStream_t stream);
 
 struct LayerNormParams {
     const void* x;

@@ -349,13 +349,30 @@ def _torch_fp32_cross(x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out, H
     return (xf + attn @ w_out.float().T + b_out.float()).cpu().numpy()
 
 
-@pytest.mark.parametrize("B,S,H,fp8", [(2, 1024, 20, False), (2, 4096, 10, True), (1, 300, 2, False)])
-def test_cross_sublayer_matches_composition_and_fp32(B, S, H, fp8):
-    x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out = _cross_inputs(B, S, H, 1100 + S, fp8=fp8)
+# The library's backend choice (AUTO) runs the query projection and the attention as one launch
+# when seq % 64 == 0, W % 128 == 0, 65 <= ctx_len <= 80 and the grid of 64 x 128 tiles is
+# resident at once (three per CU with E4M3 weights and fp16 activations, else two); each wave
+# attends with the 32 x 64 query block it projected, and the output equals the composition of the
+# individual calls bit for bit. Other shapes, and explicit backends, run the composition itself.
+@pytest.mark.parametrize("B,S,H,fp8,w8,ctx_len", [
+    (2, 1024, 20, False, False, 77),  # level 2, fused, fp16 weights
+    (2, 1024, 20, True, True, 77),    # level 2, fused, E4M3 weights and activations
+    (2, 4096, 10, False, True, 77),   # level 1, fused (640 tiles, three per CU), E4M3 weights
+    (2, 4096, 10, True, True, 77),    # level 1, E4M3 activations: 640 tiles > two per CU, composition
+    (1, 128, 2, False, True, 65),     # fused, one key in the last group
+    (1, 192, 4, False, False, 80),    # fused, 16 keys in the last group
+    (1, 300, 2, False, False, 77),    # S % 64 != 0: composition
+    (1, 256, 2, False, False, 64),    # 64 keys: composition
+])
+def test_cross_sublayer_matches_composition_and_fp32(B, S, H, fp8, w8, ctx_len):
+    x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out = _cross_inputs(B, S, H, 1100 + S, ctx_len=ctx_len,
+                                                                            fp8=w8)
     W = H * 64
-    print(f"cross sublayer B{B} S{S} H{H} fp8={fp8}", flush=True)
+    print(f"cross sublayer B{B} S{S} H{H} fp8={fp8} w8={w8} ctx{ctx_len}", flush=True)
     kv = sh.project_context_kv(ctx, w_kv)
     y = sh.cross_attn_sublayer(x, gamma, beta, w_q, w_q_scale, kv, w_out, b_out, H, fp8_activations=fp8)
+    y_flash = sh.cross_attn_sublayer(x, gamma, beta, w_q, w_q_scale, kv, w_out, b_out, H, fp8_activations=fp8,
+                                     backend=sh.FLASH_SM80)  # explicit backend: the composition
     # composition of the individual calls
     if fp8:
         codes, cs = sh.layer_norm_e4m3(x, gamma, beta)
@@ -366,18 +383,22 @@ def test_cross_sublayer_matches_composition_and_fp32(B, S, H, fp8):
     y2 = sh.linear(attn.view(-1, W), w_out, bias=b_out, residual=x.view(-1, W)).view(B, S, W)
     torch.cuda.synchronize()
     assert torch.equal(y, y2)
+    assert torch.equal(y_flash, y2)
     # oracle: the reference's block order (src/unet.cpp:508-512) with the context projected in
-    # fp32; fp8 activations (E4M3 LayerNorm output, no reference counterpart) get 4e-3 / 5e-4
-    wq = oracle.dequantize_e4m3_rows(w_q.cpu().numpy(), w_q_scale.cpu().numpy()) if fp8 else host(w_q)
+    # fp32; fp8 activations (E4M3 LayerNorm output, no reference counterpart) get 4e-3 max-abs and
+    # a mean-abs bar of 5e-4 at width 640, growing as sqrt(W / 640): the activations' 3-bit
+    # mantissa rounding accumulates over the W terms of each projected value
+    mean_fp8 = 5e-4 * (W / 640) ** 0.5
+    wq = oracle.dequantize_e4m3_rows(w_q.cpu().numpy(), w_q_scale.cpu().numpy()) if w8 else host(w_q)
     wkv = host(w_kv)
     got = host(y)
     for r0, r1 in _row_ranges(S):
         ref = oracle.cross_attn_sublayer(host(x), host(gamma), host(beta), wq, host(ctx), wkv[:W], wkv[W:],
                                          host(w_out), host(b_out), H, r0, r1, threads=THREADS)
-        assert_parity_f16_out(got[:, r0:r1], ref[:, r0:r1], 4e-3 if fp8 else 2e-3, 5e-4 if fp8 else 2e-4,
+        assert_parity_f16_out(got[:, r0:r1], ref[:, r0:r1], 4e-3 if fp8 else 2e-3, mean_fp8 if fp8 else 2e-4,
                               label=f"cross sublayer B{B} S{S} oracle rows {r0}:{r1}")
     ref = _torch_fp32_cross(x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out, H)
-    assert_parity_f16_out(got, ref, 4e-3 if fp8 else 2e-3, 5e-4 if fp8 else 2e-4,
+    assert_parity_f16_out(got, ref, 4e-3 if fp8 else 2e-3, mean_fp8 if fp8 else 2e-4,
                           label="cross sublayer vs torch fp32, all rows")
     xi = x.clone()  # in place
     sh.cross_attn_sublayer(xi, gamma, beta, w_q, w_q_scale, kv, w_out, b_out, H, out=xi, fp8_activations=fp8)
