@@ -362,11 +362,15 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
         }
     };
 
-    // Mixed workgroups: the 16 transfers of each staged head go to waves
-    // 0-3 (two K slabs each, 4 (w >> 1) + (w & 1) and that + 2) and waves
-    // 4-11 (V slab w - 4): every wave's slabs have parity w & 1, one per-lane
-    // offset per wave; k_seq % 64 == 0. The head index is a compile-time loop
-    // variable so the base pointers stay scalars.
+    // Mixed workgroups: the 16 transfers of each staged head go to the four
+    // half waves (two K slabs each: 8 + i takes slabs i and i + 4), which
+    // have one group per tile step against the whole waves' two and so slack
+    // at every barrier, and to the eight whole waves (V slab w each): the
+    // issue of a transfer holds its wave for tens of cycles, and whole waves
+    // then issue one instead of two (c3 90.9 -> 88.2 us; moving V to the half
+    // waves as well measured no faster). Every wave's slabs have parity w & 1,
+    // one per-lane offset per wave; k_seq % 64 == 0. The head index is a
+    // compile-time loop variable so the base pointers stay scalars.
     const char* set_k0 = (const char*)p.k + ((int64_t)(bh_set[0] / p.heads) * p.k_seq * p.k_row_stride +
                                              (int64_t)(bh_set[0] % p.heads) * kHeadDim) * elem;
     const char* set_k1 = (const char*)p.k + ((int64_t)(bh_set[1] / p.heads) * p.k_seq * p.k_row_stride +
@@ -375,7 +379,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                                              (int64_t)(bh_set[0] % p.heads) * kHeadDim) * elem;
     const char* set_v1 = (const char*)p.v + ((int64_t)(bh_set[1] / p.heads) * p.k_seq * p.v_row_stride +
                                              (int64_t)(bh_set[1] % p.heads) * kHeadDim) * elem;
-    const bool mixed_v = wave >= 4;
+    const bool mixed_v = wave < kMixedFull;
     const int64_t mixed_stride = mixed_v ? vs_bytes : ks_bytes;
     const uint32_t mixed_off = mixed ? lane_off(wave & 1, mixed_stride) : 0u;
     auto issue_mixed = [&](int kt, int vt) __attribute__((always_inline)) {
@@ -389,7 +393,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if (j == 1 && mixed_v) break;
-                const int slab = mixed_v ? wave - 4 : 4 * (wave >> 1) + (wave & 1) + 2 * j;
+                const int slab = mixed_v ? wave : (wave - kMixedFull) + 4 * j;
                 const char* slab_base = base + (int64_t)(tile * kKeyTile + 8 * slab) * mixed_stride;
                 lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
             }
