@@ -122,9 +122,17 @@ def time_fn(torch, fn, steps, warmup, reps=10):
     with torch.cuda.graph(graph, stream=side):
         for _ in range(reps):
             fn()
-    graph.replay()
-    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    # ~30 ms of replays first: after the host-side set-up between measurements the device has been
+    # idle and its clock needs that long to return to its loaded level (short kernels measured
+    # 5-10 % slower without it)
+    for _ in range(min(2000, int(30.0 / max(e0.elapsed_time(e1), 1e-3)) + 1)):
+        graph.replay()
+    torch.cuda.synchronize()
     e0.record()
     for _ in range(steps):
         graph.replay()
