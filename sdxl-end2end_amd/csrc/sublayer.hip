@@ -904,6 +904,7 @@ bool q_cross_attention_supported(const LinearParams& p, bool w_fp8, int compute_
     return p.m > 0 && p.seq > 0 && p.seq % 64 == 0 && p.m % p.seq == 0 && p.n % 128 == 0 && p.k % kBK == 0 &&
            p.ctx_len >= 65 && p.ctx_len <= 80 && p.kv != nullptr && p.bias == nullptr && p.residual == nullptr &&
            p.ldkv >= 2 * (int64_t)p.n && p.ldkv % 8 == 0 && ((uintptr_t)p.kv & 15) == 0 && p.ldc % 8 == 0 &&
+           (int64_t)p.ctx_len * p.ldkv * 2 <= 0x7FFFFFFF &&  // V-row transfer offsets are 32-bit
            ((uintptr_t)p.c & 15) == 0 && (int64_t)(p.m / 64) * (p.n / 128) <= 0x7FFFFFFF;
 }
 
