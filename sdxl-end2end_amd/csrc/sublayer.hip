@@ -128,17 +128,20 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 // each wave's 32 x 64 block is one 32-row query block of one head) fused
 // with the attention over kKvG 32-key groups of context (kKvHalf: the last
 // group holds at most 16 keys); see the epilogue.
-template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2, int kKvG = 0, bool kKvHalf = false>
-__global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p) {
+template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2, int kKvG = 0, bool kKvHalf = false,
+          int kWN = 2>
+__global__ __launch_bounds__(64 * kWM * kWN, kOcc) void linear_kernel(LinearParams p) {
     static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
+    static_assert(kKvG == 0 || kWN == 2, "the cross-attention form uses 128-column tiles");
     constexpr int kBMt = 64 * kTM;
-    constexpr int kWaves = 2 * kWM;            // kWM waves along M x 2 along N
+    constexpr int kBNt = 64 * kWN;             // tile columns
+    constexpr int kWaves = kWM * kWN;          // kWM waves along M x kWN along N
     constexpr int kTMw = kBMt / (32 * kWM);    // 32-row MFMA tiles per wave
     static_assert(kTMw >= 1 && kTMw * 32 * kWM == kBMt, "wave tiling");
     constexpr int kWRowBytes = kWFp8 ? 64 : kRowBytes;
     constexpr int kARowBytes = kAFp8 ? 64 : kRowBytes;
     constexpr int kATileBytes = kBMt * kARowBytes;
-    constexpr int kWTileBytes = 128 * kWRowBytes;
+    constexpr int kWTileBytes = kBNt * kWRowBytes;
     constexpr int kAXfers = kATileBytes / 1024 / kWaves;  // 1-KiB A transfers per wave and stage
     constexpr int kWXfers = kWTileBytes / 1024 / kWaves;
     static_assert(kAXfers * kWaves * 1024 == kATileBytes && kWXfers * kWaves * 1024 == kWTileBytes,
@@ -181,7 +184,7 @@ __global__ __launch_bounds__(128 * kWM, kOcc) void linear_kernel(LinearParams p)
         mb = first_m + r % rows;
         nb = r / rows;
     }
-    const int m0 = mb * kBMt, n0 = nb * kBN;
+    const int m0 = mb * kBMt, n0 = nb * kBNt;
     const int n_stages = p.k / kBK;
 
     const int64_t lda_b = kAFp8 ? p.lda : p.lda * 2;
@@ -862,6 +865,26 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
     // 2048 x 3840 x 1280 19.2 -> 16.3 and 28.2 -> 26.6 us. With fewer tiles
     // (the out-projections) they ran slower; fp16 weights (48-KiB stages, one
     // workgroup per CU) measured within 2 %, so those keep the 4-wave grids.
+    // Below 4096 rows with at least 512 columns the eight waves take 128 x 256
+    // tiles instead (2 x 4 waves): per K stage 16 KiB of A and 16 KiB of
+    // weight codes against 32 + 8 KiB for the same MFMA work, and the
+    // transfers' issue is what the loop waits on (2048 x 3840 x 1280 28.1 ->
+    // 27.4 us; 8192-row projections unchanged, so they keep 256 x 128).
+    if (w_fp8 && p.m < 4096 && p.n >= 512 &&
+        (int64_t)((p.m + 127) / 128) * ((p.n + 255) / 256) * 10 >= (int64_t)(compute_units > 0 ? compute_units : 256) * 9) {
+        p.m_blocks = (p.m + 127) / 128;
+        p.n_blocks = (p.n + 255) / 256;
+        p.group_m = 1;
+        const dim3 g8((unsigned)((int64_t)p.m_blocks * p.n_blocks)), b8(512);
+        if (a_fp8) {
+            if (nt) hipLaunchKernelGGL((linear_kernel<true, true, 2, 3, 2, true, 2, 0, false, 4>), g8, b8, 0, stream, p);
+            else hipLaunchKernelGGL((linear_kernel<true, true, 2, 3, 2, false, 2, 0, false, 4>), g8, b8, 0, stream, p);
+        } else {
+            if (nt) hipLaunchKernelGGL((linear_kernel<true, false, 2, 2, 2, true, 2, 0, false, 4>), g8, b8, 0, stream, p);
+            else hipLaunchKernelGGL((linear_kernel<true, false, 2, 2, 2, false, 2, 0, false, 4>), g8, b8, 0, stream, p);
+        }
+        return hipGetLastError();
+    }
     if (w_fp8 && (int64_t)((p.m + 255) / 256) * p.n_blocks * 10 >= (int64_t)(compute_units > 0 ? compute_units : 256) * 9) {
         p.m_blocks = (p.m + 255) / 256;
         p.group_m = p.m < 4096 ? 1 : p.m_blocks < 8 ? p.m_blocks : 8;

@@ -270,8 +270,25 @@ def test_layer_norm_e4m3(rows, width):
     assert (q.cpu().numpy() == q_ref).mean() >= 0.9999
 
 
+@pytest.mark.parametrize("M,N,K,extras", [(2048, 3840, 1280, False), (2000, 3800, 1280, True)])
+def test_linear_e4m3_wide_tiles(M, N, K, extras):
+    """E4M3 weights below 4096 rows: 128 x 256 tiles of 8 waves (2 x 4) — the level-2 QKV
+    projection, and a ragged shape (last row tile of 80, last column tile of 216) with bias and
+    residual."""
+    ab = oracle.normal_f16(1950 + M, (M, K))
+    q, s = oracle.quantize_e4m3_rows(oracle.normal_f32(1951, (N, K), 0.02))
+    bb = oracle.normal_f16(1952, (N,), 0.02) if extras else None
+    rb = oracle.normal_f16(1953, (M, N)) if extras else None
+    got = host(sh.linear(dev16(ab), torch.from_numpy(q).to(DEV), w_scale=torch.from_numpy(s).to(DEV),
+                         bias=dev16(bb) if extras else None, residual=dev16(rb) if extras else None))
+    rows = np.r_[0:256, M // 2:M // 2 + 32, M - 160:M]
+    ref = _linear_ref(ab[rows], oracle.dequantize_e4m3_rows(q, s), bb, rb[rows] if extras else None)
+    within_half_ulp(got[rows], ref, 1e-4, f"linear E4M3 {M}x{N}x{K} (128 x 256 tiles)")
+
+
 @pytest.mark.parametrize("M,N,K,extras", [(8192, 1920, 640, False), (333, 640, 640, True), (129, 200, 64, True),
-                                          (256, 1280, 1280, False)])
+                                          (256, 1280, 1280, False), (2048, 3840, 1280, False),
+                                          (2000, 3800, 1280, True)])
 def test_linear_e4m3_activations(M, N, K, extras):
     af = oracle.normal_f32(1000 + M, (M, K))
     aq, a_s = oracle.quantize_e4m3_rows(af)
