@@ -1163,9 +1163,9 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     // Work split. Three workgroups are resident per CU (occupancy 3, one wave
     // per SIMD each), S = 3 CUs slots. With U 128-row units, the rounds that
     // fill every slot run whole workgroups; the remaining R = U mod S units are
-    // re-cut so that the last round is full too: part of them becomes
+    // re-cut so that the last round is balanced: part of them becomes
     // key-split workgroups (64 rows, each wave half the keys: half the work of
-    // a whole one), 2R - S whole and 2S - 2R split (at R < S/2: 2R split).
+    // a whole one), see below.
     // The hardware deals ids x, x + CUs, x + 2 CUs to one CU, so with whole
     // workgroups first every CU of the last round gets the same mix.
     // Non-causal, unmasked calls with q_seq % 128 == 0 and k_seq % 64 == 0.
@@ -1176,7 +1176,19 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     if (compute_units > 0 && !p.causal && p.key_mask == nullptr && p.q_seq % 128 == 0 && p.k_seq % 64 == 0 &&
         p.k_seq > 0 && units % slots != 0) {
         const int64_t full = units - units % slots, rem = units % slots;
-        if (2 * rem >= slots) {
+        // Whole workgroups do more per transfer and per barrier than two
+        // key-split ones (two groups per tile step, one staging per 4 blocks):
+        // with q = rem / CUs >= 1, q whole workgroups per CU and the other
+        // rem - q CUs units as key-split ones keep the same most-loaded CU
+        // (q + 1/2 blocks per SIMD) as the all-split cut, while three
+        // workgroups per CU suffice (c1 [2,20,1024,1024] 18.5 -> 17.4 us,
+        // [2,10,2048,2048] 32.4 -> 30.5 us; below one unit per CU, whole
+        // workgroups alone measured slower).
+        const int64_t q = compute_units > 0 ? rem / compute_units : 0, r = rem - q * compute_units;
+        if (q >= 1 && q + (2 * r + compute_units - 1) / compute_units <= 3) {
+            p.whole_units = (int32_t)(full + q * compute_units);
+            p.split_units = (int32_t)(2 * r);
+        } else if (2 * rem >= slots) {
             p.whole_units = (int32_t)(full + 2 * rem - slots);
             p.split_units = (int32_t)(2 * slots - 2 * rem);
         } else {

@@ -356,7 +356,8 @@ def test_hip_graph_capture_replays():
 # Unmasked, non-causal calls with Sq % 128 == 0 and Sk % 64 == 0 fill the device's resident
 # workgroup slots with a mix of whole (128 rows, all keys) and key-split (64 rows, two waves per
 # row block on half the keys each, merged through LDS) workgroups. These shapes run all-split,
-# mixed, and mixed in a second round on an MI355X (256 CUs, 768 slots).
+# mixed, and mixed in a second round on an MI355X (256 CUs, 768 slots); with at least one leftover
+# unit per CU, whole workgroups (one or two per CU) plus key-split ones for the rest.
 
 @pytest.mark.parametrize("B,Sq,Sk,H", [
     (1, 128, 64, 1),      # one stage: each key half is 32 keys
@@ -365,7 +366,9 @@ def test_hip_graph_capture_replays():
     (1, 3584, 512, 60),   # 1680 units: two full rounds of whole workgroups, then a mixed round
     (1, 1024, 192, 8),    # 64 units -> 128 key-split workgroups, 3 key tiles
     (1, 1024, 1088, 24),  # 192 units -> 384 key-split workgroups, 17 key tiles
-    (2, 1024, 1024, 20),  # 320 units (the level-2 self-attention) -> 640 key-split workgroups
+    (2, 1024, 1024, 20),  # 320 units (the level-2 self-attention): 256 whole + 128 key-split
+    (2, 1024, 1024, 28),  # 448 units: 256 whole + 384 key-split (one or two per CU)
+    (2, 1024, 1024, 35),  # 560 units: 512 whole (two per CU) + 96 key-split
 ])
 def test_key_split_workgroups(B, Sq, Sk, H):
     qb, kb, vb = seeded(880 + Sq, B, Sq, H * 64), seeded(881 + Sk, B, Sk, H * 64), seeded(882, B, Sk, H * 64)
