@@ -181,6 +181,7 @@ __device__ __forceinline__ void store_out(T v, T* ptr) {
 // Workgroup kinds of the fused kernel.
 constexpr int kKindWhole = 0;  // 4 waves: 128 query rows, all keys
 constexpr int kKindSplit = 1;  // 4 waves: 64 query rows, each row block's keys in two halves
+constexpr int kKindSplit2 = 4;  // as kKindSplit with 64 keys of each half per stage (64 KiB of LDS)
 constexpr int kKindMixed = 2;  // 12 waves: 10 consecutive 32-row blocks, 8 whole + 2 split in groups
 constexpr int kMixedFull = 8;    // waves of a mixed workgroup that take one row block and all keys
 constexpr int kMixedBlocks = 10; // 32-row blocks per mixed workgroup
@@ -194,7 +195,8 @@ static_assert(2 * 34 * 64 * 4 + (kMixedFull + 2) * 32 * kRowBytes <= 2 * (kKRing
 template <int kWaves, bool IsBf16, bool kMaskAll, int kKind>
 __device__ __attribute__((always_inline)) inline void attention_body(const FusedAttentionParams& p,
                                                                      char (*ring)[kTileBytes]) {
-    constexpr bool split = kKind == kKindSplit;
+    constexpr bool split2 = kKind == kKindSplit2;
+    constexpr bool split = kKind == kKindSplit || split2;  // row assignment, merge and epilogue
     constexpr bool mixed = kKind == kKindMixed;
     constexpr int kBlockQueries = kWaves * 32;
     constexpr int kLoadsPerWave = 16 / kWaves;  // 1-KiB transfers per wave and tile (K and V), 4-wave kinds
@@ -294,7 +296,8 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     // Key-split calls: stage t holds keys 32t .. +31 of each half (rows 0-31
     // half 0, rows 32-63 half 1); k_seq % 64 == 0.
     const int half_keys = p.k_seq / 2;
-    const int n_tiles = (split || mixed) ? p.k_seq / kKeyTile : (n_keys + kKeyTile - 1) / kKeyTile;
+    const int n_tiles = split2 ? p.k_seq / (2 * kKeyTile)
+                               : (split || mixed) ? p.k_seq / kKeyTile : (n_keys + kKeyTile - 1) / kKeyTile;
     // Tiles [0, n_plain) are complete and need no mask (kMaskAll covers key-mask
     // and causal calls, where every tile is masked).
     const int n_plain = kMaskAll ? 0 : n_keys / kKeyTile;
@@ -358,6 +361,25 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             const int slab = 2 * j + (wave & 1), half = slab >> 2;
             const char* slab_base =
                 (is_v ? vbase : kbase) + (int64_t)(half * half_keys + 32 * tile + 8 * (slab & 3)) * whole_stride;
+            lds_dma16(slab_base, whole_off, lds_addr(buf + 8 * slab * kRowBytes));
+        }
+    };
+
+    // Key-split stages of 64 keys per half (split2): stage t holds keys
+    // 64t .. +63 of half 0 in rows 0-63 and of half 1 in rows 64-127 of a
+    // 128-row buffer (two consecutive tiles); slab n covers rows 8n .. 8n+7.
+    auto issue_split2 = [&](int kt, int vt) __attribute__((always_inline)) {
+        const bool is_v = wave >= 2;
+        const int tile = is_v ? vt : kt;
+        if (tile < 0 || tile >= n_tiles) return;
+        // byte offset, not an indexed choice of buffers (which the compiler
+        // turned into a pointer table in scratch, read under vmcnt waits)
+        const char* buf = &ring[0][0] + (2 * ((is_v ? kKRing : 0) + (tile & 1))) * kTileBytes;
+#pragma unroll
+        for (int j = 0; j < 2 * kLoadsPerWave; ++j) {
+            const int slab = 2 * j + (wave & 1), half = slab >> 3;
+            const char* slab_base =
+                (is_v ? vbase : kbase) + (int64_t)(half * half_keys + 64 * tile + 8 * (slab & 7)) * whole_stride;
             lds_dma16(slab_base, whole_off, lds_addr(buf + 8 * slab * kRowBytes));
         }
     };
@@ -618,7 +640,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     // and two V buffers suffice. sa/sb: scores of groups 0/1.
     f32x16 sa, sb;
     i16x8 kop[4];
-    if constexpr (split) {
+    if constexpr (split && !split2) {
         // ---- key-split workgroup: one 32-key group per stage and wave (group
         // khalf of the stage buffers). The group after next lies in a stage not
         // yet resident, so each stage loads the next group's K operands at its
@@ -650,6 +672,41 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                 stage.template operator()<false, false>(t + 1);
             }
             if (t < n_tiles) stage.template operator()<false, true>(t);
+        }
+    } else if constexpr (split2) {
+        // ---- key-split workgroup with 64 keys of each half per stage: each
+        // wave steps through two groups per stage as a whole wave does (its
+        // half's rows of the 128-row stage buffers), so the K operands of the
+        // group after next are prefetched across stages as in the whole kind.
+        const int hrow = khalf * 64 * kRowBytes;
+        issue_split2(0, 0);
+        issue_split2(1, -1);
+        wait_vmem_all();
+        __syncthreads();
+        load_k(&ring[0][0] + hrow, 0, kop);
+        sa = mfma32<IsBf16>(kop[0], qop[0], neg_m);
+#pragma unroll
+        for (int ks = 1; ks < 4; ++ks) sa = mfma32<IsBf16>(kop[ks], qop[ks], sa);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sa[i] *= c;  // exp2 arguments of the first group
+        load_k(&ring[0][0] + hrow, 1, kop);
+        auto stage2 = [&]<bool kFirst, bool kOdd>(int t) __attribute__((always_inline)) {
+            wait_vmem_all();  // this lane's transfers of K(t+1), V(t) landed
+            __syncthreads();  // ... and every lane's; stage t-1 fully consumed
+            issue_split2(t + 2, t + 1);
+            const char* v_t = &ring[2 * (kKRing + (kOdd ? 1 : 0))][0] + hrow;
+            const char* k_t1 = &ring[2 * (kOdd ? 0 : 1)][0] + hrow;
+            group_step.template operator()<false, kFirst>(sa, sb, kop, v_t, 0, t, ~0ull, k_t1, 0, true);
+            group_step.template operator()<false, false>(sb, sa, kop, v_t, 1, t, ~0ull, k_t1, 1, true);
+        };
+        int t = 0;
+        if (n_tiles > 0) {
+            stage2.template operator()<true, false>(0);
+            for (t = 1; t + 1 < n_tiles; t += 2) {
+                stage2.template operator()<false, true>(t);
+                stage2.template operator()<false, false>(t + 1);
+            }
+            if (t < n_tiles) stage2.template operator()<false, true>(t);
         }
     } else if constexpr (mixed) {
         // ---- mixed workgroup: whole waves step through both groups of every
@@ -842,6 +899,18 @@ __global__ __launch_bounds__(kWaves * 64, 3) void fused_attention_d64_kernel(Fus
         }
     }
     attention_body<kWaves, IsBf16, kMaskAll, kKindWhole>(p, ring);
+}
+
+// Whole workgroups with split2 key-split ones (64 KiB of LDS: two per CU),
+// for single-round grids of at most two workgroups per CU.
+template <bool IsBf16>
+__global__ __launch_bounds__(4 * 64, 2) void fused_attention_d64_wide_kernel(FusedAttentionParams p) {
+    __shared__ __attribute__((aligned(16))) char ring[2 * (kKRing + kVRing)][kTileBytes];
+    if ((int)blockIdx.x >= p.whole_units) {
+        attention_body<4, IsBf16, false, kKindSplit2>(p, ring);
+        return;
+    }
+    attention_body<4, IsBf16, false, kKindWhole>(p, ring);
 }
 
 // Mixed workgroups: 12 waves, one workgroup per CU; K and V rings for up to
@@ -1171,6 +1240,7 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     // Non-causal, unmasked calls with q_seq % 128 == 0 and k_seq % 64 == 0.
     p.whole_units = p.total_blocks;
     p.split_units = 0;
+    bool wide = false;  // whole + split2 workgroups on the 64-KiB kernel
     const int64_t slots = (int64_t)compute_units * 3;
     const int64_t units = p.total_blocks;
     if (compute_units > 0 && !p.causal && p.key_mask == nullptr && p.q_seq % 128 == 0 && p.k_seq % 64 == 0 &&
@@ -1188,6 +1258,9 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
         if (q >= 1 && q + (2 * r + compute_units - 1) / compute_units <= 3) {
             p.whole_units = (int32_t)(full + q * compute_units);
             p.split_units = (int32_t)(2 * r);
+            // one round of at most two workgroups per CU: key-split workgroups
+            // with 64 keys of each half per stage
+            wide = full == 0 && q == 1 && 2 * r <= compute_units && p.k_seq % 128 == 0;
         } else if (2 * rem >= slots) {
             p.whole_units = (int32_t)(full + 2 * rem - slots);
             p.split_units = (int32_t)(2 * slots - 2 * rem);
@@ -1219,6 +1292,11 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
         }
     }
     const dim3 grid(p.whole_units + p.split_units), block(64 * kFusedWaves);
+    if (wide) {
+        if (is_bf16) hipLaunchKernelGGL((fused_attention_d64_wide_kernel<true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((fused_attention_d64_wide_kernel<false>), grid, block, 0, stream, p);
+        return hipGetLastError();
+    }
     if (is_bf16) {
         if (mask_all) hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, true>), grid, block, 0, stream, p);
         else hipLaunchKernelGGL((fused_attention_d64_kernel<kFusedWaves, true, false>), grid, block, 0, stream, p);

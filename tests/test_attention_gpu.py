@@ -366,7 +366,8 @@ def test_hip_graph_capture_replays():
     (1, 3584, 512, 60),   # 1680 units: two full rounds of whole workgroups, then a mixed round
     (1, 1024, 192, 8),    # 64 units -> 128 key-split workgroups, 3 key tiles
     (1, 1024, 1088, 24),  # 192 units -> 384 key-split workgroups, 17 key tiles
-    (2, 1024, 1024, 20),  # 320 units (the level-2 self-attention): 256 whole + 128 key-split
+    (2, 1024, 1024, 20),  # 320 units (the level-2 self-attention): 256 whole + 128 key-split with
+                          # 64 keys per half per stage (64 KiB kernel, two workgroups per CU)
     (2, 1024, 1024, 28),  # 448 units: 256 whole + 384 key-split (one or two per CU)
     (2, 1024, 1024, 35),  # 560 units: 512 whole (two per CU) + 96 key-split
 ])
