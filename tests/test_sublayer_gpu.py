@@ -210,7 +210,7 @@ def check_vs_oracle_sublayer(y, x, gamma, beta, q8, s8, w_out, b_out, H, label, 
         assert_parity_f16_out(got[:, r0:r1], ref[:, r0:r1], max_abs, mean_abs, label=f"{label} oracle rows {r0}:{r1}")
 
 
-@pytest.mark.parametrize("B,S,H", [(2, 4096, 10), (1, 300, 2)])
+@pytest.mark.parametrize("B,S,H", [(2, 4096, 10), (2, 1024, 20), (1, 300, 2)])
 def test_sublayer_matches_composition_and_oracle(B, S, H):
     x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(B, S, H, 960 + S)
     W = H * 64
@@ -306,7 +306,7 @@ def test_linear_e4m3_activations(M, N, K, extras):
     within_half_ulp(got[rows], ref, 1e-4, f"linear E4M3 x E4M3 {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("B,S,H", [(2, 4096, 10), (1, 300, 2)])
+@pytest.mark.parametrize("B,S,H", [(2, 4096, 10), (2, 1024, 20), (1, 300, 2)])
 def test_sublayer_fp8_activations(B, S, H):
     x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(B, S, H, 1010 + S)
     W = H * 64
@@ -321,10 +321,12 @@ def test_sublayer_fp8_activations(B, S, H):
     assert torch.equal(y, y2)
     # The E4M3 rounding of the LayerNorm output (3 mantissa bits; no reference counterpart: its
     # FP8 path is weight-only) enters q, k, v at about 2% relative and is damped by the softmax
-    # averaging and the 0.02-scale output projection: bar 4e-3 beyond the output rounding and
-    # 3e-4 mean against the oracle's unquantised activations.
+    # averaging and the 0.02-scale output projection: bar 4e-3 beyond the output rounding and a
+    # mean of 3e-4 up to width 640 against the oracle's unquantised activations, times W / 640 above:
+    # the rounding reaches the output through two W-term sums (the q|k|v projection, then the
+    # out-projection), measured 5.2e-4 at width 1280.
     check_vs_oracle_sublayer(y, x, gamma, beta, q8, s8, w_out, b_out, H, f"sublayer fp8 act B{B} S{S}",
-                             max_abs=4e-3, mean_abs=3e-4)
+                             max_abs=4e-3, mean_abs=3e-4 * max(1.0, W / 640))
 
 
 # ---------------------------------------------------------------- cross-attention sublayer
@@ -403,9 +405,9 @@ def test_cross_sublayer_matches_composition_and_fp32(B, S, H, fp8, w8, ctx_len):
     assert torch.equal(y_flash, y2)
     # oracle: the reference's block order (src/unet.cpp:508-512) with the context projected in
     # fp32; fp8 activations (E4M3 LayerNorm output, no reference counterpart) get 4e-3 max-abs and
-    # a mean-abs bar of 5e-4 at width 640, growing as sqrt(W / 640): the activations' 3-bit
+    # a mean-abs bar of 5e-4 up to width 640, growing as sqrt(W / 640) above: the activations' 3-bit
     # mantissa rounding accumulates over the W terms of each projected value
-    mean_fp8 = 5e-4 * (W / 640) ** 0.5
+    mean_fp8 = 5e-4 * max(1.0, W / 640) ** 0.5
     wq = oracle.dequantize_e4m3_rows(w_q.cpu().numpy(), w_q_scale.cpu().numpy()) if w8 else host(w_q)
     wkv = host(w_kv)
     got = host(y)
