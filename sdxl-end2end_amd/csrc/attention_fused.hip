@@ -209,8 +209,10 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
     // Workgroup kinds. Whole: 128 query rows (4 waves x 32), all keys.
     // Key-split (ids >= whole_units): 64 query rows; wave w takes rows
     // 32 (w & 1) .. +31 and key half w >> 1, and the two halves of each row
-    // block are merged through LDS at the end. Mixing the kinds lets a call
-    // fill every resident workgroup slot with equal work (see the launcher).
+    // block are merged through LDS at the end (split2, in the 64-KiB kernel:
+    // each stage holds 64 keys of each half, so a wave steps through two
+    // groups per stage as a whole wave does). Mixing the kinds lets a call
+    // fill the resident workgroup slots evenly (see the launcher).
     // Mixed (one 12-wave workgroup per CU, three waves per SIMD): row blocks
     // 10i .. 10i + 9 of the flattened (batch, head, block) order; waves 0-7
     // take blocks 10i + w with all keys, waves 8-11 take blocks 10i + 8 + (w-8)/2
