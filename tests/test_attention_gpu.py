@@ -361,7 +361,7 @@ def test_hip_graph_capture_replays():
 
 @pytest.mark.parametrize("B,Sq,Sk,H", [
     (1, 128, 64, 1),      # one stage: each key half is 32 keys
-    (1, 256, 512, 2),     # 4 units -> 8 key-split workgroups
+    (1, 256, 512, 2),     # 4 units -> 8 key-split workgroups (64 keys per half per stage)
     (2, 384, 1088, 3),    # 18 units, Sk not a multiple of 128
     (1, 3584, 512, 60),   # 1680 units: two full rounds of whole workgroups, then a mixed round
     (1, 1024, 192, 8),    # 64 units -> 128 key-split workgroups, 3 key tiles
@@ -503,14 +503,18 @@ def torch_reference_bf16(q, k, v, heads):
 # rescale of O and l, shift of the next group's partial scores) only when a half's probability
 # sum exceeds 2^14 or is not finite, i.e. when logits rise ~14 log2 units above the anchor set by
 # the first group. N(0,1) inputs at scale 1/8 never get there; these inputs do, on every kernel
-# kind: whole 4-wave workgroups (ragged Sq), the key-split grid ([2,20,1024,64], configs[0]'s
-# shape), the mixed 12-wave grid ([2,10,4096,64], configs[2]'s shape). Semantics followed:
+# kind: whole 4-wave workgroups (ragged Sq), whole + key-split workgroups with 64 keys per half
+# per stage ([2,20,1024,64], configs[0]'s shape), key-split workgroups alone of that kind
+# ([1,10,1024,64]), whole + key-split workgroups with 32 keys per half per stage ([2,28,1024,64]),
+# the mixed 12-wave grid ([2,10,4096,64], configs[2]'s shape). Semantics followed:
 # src/unet.cpp:458-470 (exact max-subtract) and src/cuda/flash_attention_sm80.cu:141-173 (online
 # rescale); the bar is the same 2e-3 / 2e-4 against the FP32 oracle.
 
 ANCHOR_SHAPES = {
     "whole": (1, 1000, 1000, 2),       # Sq % 128 != 0: whole workgroups only, ragged last tile
     "key_split": (2, 1024, 1024, 20),  # 1280 row blocks on 256 CUs: whole + key-split grid
+    "split_only": (1, 1024, 1024, 10),  # 80 units: key-split workgroups only
+    "key_split_32": (2, 1024, 1024, 28),  # 448 units: whole + 384 key-split (32 keys per half)
     "mixed": (2, 4096, 4096, 10),      # 2560 row blocks: mixed 12-wave workgroups
 }
 
@@ -569,7 +573,7 @@ def test_large_logits_anchor_update(grid, kind):
         assert np.abs(got - vrow).max() <= 1e-6  # fp16 V values, reproduced exactly
 
 
-@pytest.mark.parametrize("grid", ["whole", "key_split", "mixed"])
+@pytest.mark.parametrize("grid", list(ANCHOR_SHAPES))
 def test_large_logits_anchor_update_bf16(grid):
     B, Sq, Sk, H = ANCHOR_SHAPES[grid]
     qf = oracle.normal_f32(1200, (B, Sq, H * 64), 16.0)
