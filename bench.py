@@ -192,6 +192,16 @@ def bench_sublayer(torch, sh, steps=50, warmup=5, B=2, S=4096, H=10):
             e["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
             e["mfma_frac"] = round(fl / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
         out["stages"][name] = e
+    if W == 640:
+        # LayerNorm inside the q|k|v projection (sdxl_layer_norm_linear): replaces the first two stages
+        fl, by = sh.linear_flops(M, 3 * W, W), 2.0 * M * W + 3 * W * W + 2.0 * M * 3 * W
+        t = time_fn(torch, lambda: sh.layer_norm_linear(x.view(M, W), gamma, beta, q8, s8, out=qkv), steps, warmup)
+        out["layer_norm_qkv_fused"] = {"us": round(t * 1e3, 2), "hbm_gbs": round(by / (t * 1e-3) / 1e9, 1),
+                                       "tflops": round(fl / (t * 1e-3) / 1e12, 1),
+                                       "mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)}
+        t = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws,
+                                                    ln_fusion=False), steps, warmup)
+        out["fused_call_separate_ln_us"] = round(t * 1e3, 2)
     ms = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws),
                  steps, warmup)
     out["sum_of_stages_us"] = round(total * 1e3, 2)

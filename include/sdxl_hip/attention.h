@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define SDXL_HIP_ABI_VERSION 1
+#define SDXL_HIP_ABI_VERSION 2
 
 typedef enum sdxl_status {
     SDXL_STATUS_OK = 0,

@@ -85,6 +85,20 @@ sdxl_status sdxl_linear_e4m3(const sdxl_linear_desc* desc, const uint8_t* a, con
 sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, uint8_t* q, float* scales,
                                     void* stream);
 
+/* LayerNorm fused into the projection that consumes it, for the transformer
+ * block's norm1 -> q|k|v (reference src/cuda/unet.cpp:106-112: Ops::layer_norm,
+ * src/cuda/ops_kernels.cu:1428-1460, then Ops::linear on FP8 weights,
+ * src/cuda/fp8_kernels.cu:52-245): c = LN(x) . w^T * w_scale (+ bias), with LN(x)
+ * rounded to fp16 exactly as sdxl_layer_norm rounds it and the same fp32 sums as
+ * sdxl_linear, so c equals sdxl_layer_norm followed by sdxl_linear bit for bit;
+ * the normalised rows never reach HBM. desc as sdxl_linear (k = width, a_row_stride
+ * = x row stride; w_dtype must be SDXL_DTYPE_E4M3; residual_row_stride 0). eps 0
+ * means 1e-5. SDXL_STATUS_UNSUPPORTED unless k == 640, n % 128 == 0, 16-byte
+ * aligned x rows, gamma, beta and w rows, 8-byte aligned c rows. */
+sdxl_status sdxl_layer_norm_linear(const sdxl_linear_desc* desc, const void* x, const void* gamma,
+                                   const void* beta, float eps, const void* w, const float* w_scale,
+                                   const void* bias, void* c, void* stream);
+
 typedef struct sdxl_sublayer_desc {
     int64_t batch;
     int64_t seq;
@@ -97,6 +111,10 @@ typedef struct sdxl_sublayer_desc {
      * output per row and the projection runs on the fp8 matrix cores; needs E4M3
      * w_qkv). */
     int32_t qkv_activations;
+    /* 0: the LayerNorm runs inside the q|k|v projection (sdxl_layer_norm_linear)
+     * where that kernel takes the shape (fp16 activations, E4M3 w_qkv, width 640),
+     * else as its own launch; 1: always its own launch. Same results either way. */
+    int32_t ln_fusion;
 } sdxl_sublayer_desc;
 
 /* Workspace the sublayer needs: batch * seq * width * 8 bytes (normalised

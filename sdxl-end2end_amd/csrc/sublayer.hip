@@ -32,6 +32,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "sublayer_kernels.hpp"
 
 namespace sdxl_hip {
@@ -620,6 +622,7 @@ __device__ __forceinline__ float wave_max(float x) {
 
 template <int kPer, bool kE4M3, bool kNt>
 __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
+#pragma clang fp contract(off)  // every operation rounded on its own, as the reference's CPU LayerNorm
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= p.rows) return;  // wave-uniform; no barrier in this kernel
@@ -639,8 +642,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
         v[2 * j + 1] = ok ? (float)h[j][1] : 0.0f;
         sum += v[2 * j] + v[2 * j + 1];
     }
-    const float inv_w = 1.0f / (float)p.width;
-    const float mean = wave_sum(sum) * inv_w;
+    const float mean = wave_sum(sum) / (float)p.width;
     float sq = 0.0f;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
@@ -649,7 +651,7 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
             sq += d0 * d0 + d1 * d1;
         }
     }
-    const float var = fmaxf(wave_sum(sq) * inv_w, 0.0f);
+    const float var = fmaxf(wave_sum(sq) / (float)p.width, 0.0f);
     const float inv = 1.0f / sqrtf(var + p.eps);
     if constexpr (kE4M3) {
         float yv[2 * kPer];
@@ -704,17 +706,14 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
 // and stores), otherwise as layer_norm_kernel (same two-pass centred variance,
 // fp32 maths, one rounding). kChunks = ceil(width / 512).
 typedef _Float16 f16x8v __attribute__((ext_vector_type(8)));
-template <int kChunks, bool kNt, bool kE4M3>
-__global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= p.rows) return;  // wave-uniform; no barrier in this kernel
-    const int chunks = p.width / 8;
-    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + row * p.ldx);
-    f16x8v h[kChunks];
-#pragma unroll
-    for (int j = 0; j < kChunks; ++j) h[j] = x[min(lane + 64 * j, chunks - 1)];
-    float v[8 * kChunks];
+// Two-pass statistics of one row held as 16-byte chunks (lane l: chunks l,
+// l + 64, ..; chunks past the row masked to zero): the values in fp32, the
+// mean and 1 / sqrt(var + eps). Shared by the LayerNorm kernels so that every
+// LayerNorm in this file rounds identically.
+template <int kChunks>
+__device__ __forceinline__ void ln_row_stats_v8(const f16x8v (&h)[kChunks], int lane, int chunks, int width, float eps,
+                                                float (&v)[8 * kChunks], float& mean, float& inv) {
+#pragma clang fp contract(off)  // every operation rounded on its own, as the reference's CPU LayerNorm
     float sum = 0.0f;
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
@@ -725,8 +724,7 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
             sum += v[8 * j + e];
         }
     }
-    const float inv_w = 1.0f / (float)p.width;
-    const float mean = wave_sum(sum) * inv_w;
+    mean = wave_sum(sum) / (float)width;
     float sq = 0.0f;
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
@@ -738,8 +736,40 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
             }
         }
     }
-    const float var = fmaxf(wave_sum(sq) * inv_w, 0.0f);
-    const float inv = 1.0f / sqrtf(var + p.eps);
+    const float var = fmaxf(wave_sum(sq) / (float)width, 0.0f);
+    inv = 1.0f / sqrtf(var + eps);
+}
+
+// One normalised value in fp32: ((v - mean) * inv) * gamma + beta, each
+// operation rounded on its own (no fused multiply-add), as the reference's CPU
+// LayerNorm computes it.
+__device__ __forceinline__ float ln_affine(float v, float mean, float inv, _Float16 g, _Float16 b) {
+#pragma clang fp contract(off)
+    return (v - mean) * inv * (float)g + (float)b;
+}
+
+// One normalised chunk, rounded once to fp16.
+__device__ __forceinline__ f16x8v ln_out_v8(const float* v, float mean, float inv, f16x8v gg, f16x8v bb) {
+#pragma clang fp contract(off)
+    f16x8v o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (_Float16)ln_affine(v[e], mean, inv, gg[e], bb[e]);
+    return o;
+}
+
+template <int kChunks, bool kNt, bool kE4M3>
+__global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.rows) return;  // wave-uniform; no barrier in this kernel
+    const int chunks = p.width / 8;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + row * p.ldx);
+    f16x8v h[kChunks];
+#pragma unroll
+    for (int j = 0; j < kChunks; ++j) h[j] = x[min(lane + 64 * j, chunks - 1)];
+    float v[8 * kChunks];
+    float mean, inv;
+    ln_row_stats_v8<kChunks>(h, lane, chunks, p.width, p.eps, v, mean, inv);
     const f16x8v* g = (const f16x8v*)p.gamma;
     const f16x8v* bt = (const f16x8v*)p.beta;
     if constexpr (kE4M3) {
@@ -751,7 +781,7 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
             const int c = min(lane + 64 * j, chunks - 1);
             const f16x8v gg = g[c], bb = bt[c];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) v[8 * j + e] = (v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e];
+            for (int e = 0; e < 8; ++e) v[8 * j + e] = ln_affine(v[8 * j + e], mean, inv, gg[e], bb[e]);
             if (lane + 64 * j < chunks)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[8 * j + e]));
@@ -784,13 +814,235 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
     for (int j = 0; j < kChunks; ++j) {
         const int c = lane + 64 * j;
         if (c < chunks) {
-            const f16x8v gg = g[c], bb = bt[c];
-            f16x8v o;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (_Float16)((v[8 * j + e] - mean) * inv * (float)gg[e] + (float)bb[e]);
-            store_out<kNt>(o, y + c);
+            store_out<kNt>(ln_out_v8(v + 8 * j, mean, inv, g[c], bt[c]), y + c);
         }
     }
+}
+
+// LayerNorm fused into the projection that consumes it, for K = kK input
+// features and E4M3 weights (the transformer block's norm1 -> q|k|v at level 1,
+// src/cuda/unet.cpp:106-112): c[m, n] = w_scale[n] * sum_k LN(x)[m, k] w[n, k]
+// (+ bias[n]), with LN(x) exactly as the LayerNorm kernel rounds it to fp16.
+//
+// One workgroup of 8 waves per CU (two per SIMD) owns 64 rows and a range of
+// 128-column chunks of the output. Prologue: the rows are normalised once
+// (one wave per row, the LayerNorm kernel's arithmetic) into LDS, then each
+// wave takes its 32 rows' normalised values into registers as MFMA operands
+// (kK / 16 steps of 8 values: 160 VGPRs at kK = 640), so the activations
+// never go back to HBM and are read from LDS once. Main loop: the E4M3 weight
+// rows of each chunk stream HBM/L2 -> LDS by global_load_lds_dwordx4 in
+// 128-column K stages (two 64-byte-row sub-stages, linear_kernel's layout)
+// through a ring of three (prefetch distance two, one barrier per stage);
+// wave (wm, wn) computes rows 32 wm .. +31 x columns 32 wn .. +31 of a chunk
+// as one chain of kK / 16 v_mfma_f32_32x32x16_f16 over linear_kernel's K
+// order, operand layouts and code decode, so the fp32 sums equal that
+// kernel's. A chunk's output is written (LDS-staged, 64-byte row segments)
+// during the next chunk's second stage, so the stores drain under MFMA work
+// instead of in one burst at the end. Per-column scales and bias sit in LDS,
+// and every lane stores (rows past m repeat row m - 1 with its own value), so
+// the vector-memory operations in the loop are a fixed sequence and every
+// wait counts exactly the transfers it needs.
+constexpr int kLnLinMaxCols = 2048;  // output columns per workgroup (scales and bias in LDS)
+
+template <int kK, bool kNt>
+__global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
+    constexpr int kStages = kK / 128;        // 128-column K stages per chunk
+    constexpr int kSteps = kK / 16;          // MFMA K steps
+    constexpr int kStageBytes = 2 * 128 * 64;  // two sub-stages of 128 code rows x 64 bytes
+    constexpr int kRing = 3;
+    constexpr int kARow = 2 * kK;            // one normalised row, bytes
+    constexpr int kLnChunks = (kK / 8 + 63) / 64;
+    static_assert(kK % 128 == 0, "128-column K stages; the operand swizzle works on groups of 16 chunks");
+    static_assert(8 * 32 * 128 <= 64 * kARow, "epilogue staging fits in the row buffer");
+    __shared__ __attribute__((aligned(16))) char ring[kRing][kStageBytes];
+    __shared__ __attribute__((aligned(16))) char abuf[64 * kARow];
+    __shared__ __attribute__((aligned(16))) float sc_lds[kLnLinMaxCols];
+    __shared__ __attribute__((aligned(16))) float bias_lds[kLnLinMaxCols];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int hf = lane >> 5, col = lane & 31;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    // XCD-aware task order (as linear_kernel): the n_split tasks of a row block
+    // are consecutive, so they run on one XCD and share its rows in L2.
+    int task;
+    {
+        const int n = p.m_blocks * p.n_split;
+        const int id = blockIdx.x;
+        const int xcd = id & 7, slot = id >> 3;
+        const int per = n >> 3, extra = n & 7;
+        task = xcd * per + (xcd < extra ? xcd : extra) + slot;
+    }
+    const int mb = task / p.n_split, ns = task % p.n_split;
+    const int m0 = mb * 64;
+    const int c_begin = (int)((int64_t)ns * p.chunks / p.n_split);
+    const int c_end = (int)((int64_t)(ns + 1) * p.chunks / p.n_split);
+    const int nch = c_end - c_begin;  // >= 1: n_split <= chunks
+    const int G = nch * kStages;      // K stages of the workgroup
+
+    // Weight transfers of stage g (chunk c_begin + g / kStages, K stage
+    // g % kStages): wave w moves code rows 16 w .. +15 of both sub-stages;
+    // lane l takes row 16 w + l / 4 and global chunk (l % 4) ^ ((row >> 2) & 3),
+    // the slot the readers expect, so its offset is the same for every stage.
+    const int dma_row = 16 * wave + (lane >> 2);
+    const uint32_t w_lane_off =
+        (uint32_t)(dma_row * p.ldw) + (uint32_t)(((lane & 3) ^ ((dma_row >> 2) & 3)) << 4);
+    auto issue_stage = [&](int g) __attribute__((always_inline)) {
+        const int chunk = c_begin + g / kStages, st = g % kStages;
+        const char* base = (const char*)p.w + (int64_t)chunk * 128 * p.ldw + st * 128;
+        char* buf = ring[g % kRing];
+        lds_dma16(base, w_lane_off, lds_addr(buf + wave * 1024));
+        lds_dma16(base + 64, w_lane_off, lds_addr(buf + 8192 + wave * 1024));
+    };
+    issue_stage(0);
+    if (G > 1) issue_stage(1);
+
+    // Per-column scales and bias of the workgroup's columns, once.
+    {
+        const int n0 = c_begin * 128, ncols = nch * 128;
+        for (int i = threadIdx.x; i < ncols; i += 512) {
+            sc_lds[i] = p.w_scale[n0 + i];
+            bias_lds[i] = p.bias != nullptr ? (float)((const _Float16*)p.bias)[n0 + i] : 0.0f;
+        }
+    }
+
+    // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7; rows past
+    // m repeat row m - 1). Row r's 16-byte chunk c sits at slot c ^ (r & 15).
+    {
+        constexpr int kChunks = kK / 8;
+        const f16x8v* g = (const f16x8v*)p.gamma;
+        const f16x8v* bt = (const f16x8v*)p.beta;
+        f16x8v gg[kLnChunks], bb[kLnChunks];
+#pragma unroll
+        for (int j = 0; j < kLnChunks; ++j) {
+            gg[j] = g[min(lane + 64 * j, kChunks - 1)];
+            bb[j] = bt[min(lane + 64 * j, kChunks - 1)];
+        }
+        f16x8v h[8][kLnChunks];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int gm = min(m0 + 8 * wave + i, p.m - 1);
+            const f16x8v* xr = (const f16x8v*)((const _Float16*)p.x + (int64_t)gm * p.ldx);
+#pragma unroll
+            for (int j = 0; j < kLnChunks; ++j) h[i][j] = xr[min(lane + 64 * j, kChunks - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 8 * wave + i;
+            float v[8 * kLnChunks];
+            float mean, inv;
+            ln_row_stats_v8<kLnChunks>(h[i], lane, kChunks, kK, p.eps, v, mean, inv);
+#pragma unroll
+            for (int j = 0; j < kLnChunks; ++j) {
+                const int c = lane + 64 * j;
+                if (c < kChunks)
+                    *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) =
+                        ln_out_v8(v + 8 * j, mean, inv, gg[j], bb[j]);
+            }
+        }
+    }
+    __syncthreads();
+    // Activation operands of the wave's rows: step ks = 4 s + 2 pp + q (s: 64-column
+    // sub-stage) takes columns 64 s + 32 pp + 16 hf + 8 q .. +7 (linear_kernel's K order).
+    i16x8 aop[kSteps];
+    {
+        const int ar = 32 * wm + col;
+#pragma unroll
+        for (int ks = 0; ks < kSteps; ++ks) {
+            const int c = 8 * (ks >> 2) + 4 * ((ks >> 1) & 1) + 2 * hf + (ks & 1);
+            aop[ks] = *(const lds_i16x8*)(abuf + ar * kARow + ((c ^ (ar & 15)) << 4));
+        }
+    }
+    __syncthreads();  // the row buffer becomes the epilogue staging
+
+    const int wr = 32 * wn + col;  // weight row of this lane within a chunk
+    const int w_off = wr * 64, w_swz = (wr >> 2) & 3;
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+    char* stg = abuf + wave * (32 * 128);
+    // Epilogue of one chunk's 32 x 32 block, in two parts: park() writes it
+    // row-major to the wave's LDS staging at the end of the chunk (128-byte fp32
+    // rows, chunk c of row r at c ^ (r & 7); acc[4u + q] is row col, column
+    // 8u + 4hf + q), store() reads it back during the next chunk with lane l on
+    // columns 4 (l % 8) .. +3 of rows l / 8 + 8 it, scales, adds the bias,
+    // rounds and stores: exactly four stores per lane.
+    auto park = [&](const f32x16& a) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            *(lds_f32x4*)(stg + col * 128 + (((2 * u + hf) ^ (col & 7)) << 4)) =
+                f32x4{a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3]};
+    };
+    auto store = [&](int ci) __attribute__((always_inline)) {
+        const int lc = ci * 128 + 32 * wn + 4 * (lane & 7);  // column within the workgroup's range
+        const f32x4 e_scale = *(const lds_f32x4*)(sc_lds + lc);
+        const f32x4 e_bias = *(const lds_f32x4*)(bias_lds + lc);
+        const int en = c_begin * 128 + lc;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int r = (lane >> 3) + 8 * it;
+            const int m = min(m0 + 32 * wm + r, p.m - 1);
+            const f32x4 v = *(const lds_f32x4*)(stg + r * 128 + (((lane & 7) ^ (r & 7)) << 4));
+            // fp32 value first (one fused multiply-add), then fp16, as
+            // linear_kernel's epilogue rounds: the empty asm keeps the compiler
+            // from rounding the fma straight to fp16 (v_fma_mix) in one step
+            f32x4 o = {__builtin_fmaf(v[0], e_scale[0], e_bias[0]), __builtin_fmaf(v[1], e_scale[1], e_bias[1]),
+                       __builtin_fmaf(v[2], e_scale[2], e_bias[2]), __builtin_fmaf(v[3], e_scale[3], e_bias[3])};
+            asm volatile("" : "+v"(o));
+            store_out<kNt>(f16x4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]},
+                           (f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en));
+        }
+    };
+
+    // Waits before stage g: the vector-memory operations issued after stage
+    // g's transfers are stage g + 1's two transfers (when it exists) and, in
+    // K stages 2 and 3 of every chunk but the first, the previous chunk's four
+    // output stores (issued in K stage 1): vmcnt counts them in issue order.
+    auto wait_stage = [&](bool next, bool stores) __attribute__((always_inline)) {
+        if (stores) {
+            if (next) wait_vmem<6>();
+            else wait_vmem<4>();
+        } else {
+            if (next) wait_vmem<2>();
+            else wait_vmem<0>();
+        }
+    };
+
+    for (int ci = 0; ci < nch; ++ci) {
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < kStages; ++st) {
+            const int g = ci * kStages + st;
+            wait_stage(g + 1 < G, ci > 0 && (st == 2 || st == 3));
+            __syncthreads();  // stage g landed for every wave; stage g - 1's buffer is free
+            if (g + 2 < G) issue_stage(g + 2);
+            const char* cur = ring[g % kRing];
+            auto read_w = [&](int pr) __attribute__((always_inline)) {
+                return *(const lds_u32x4*)(cur + (pr >> 1) * 8192 + w_off + (((2 * (pr & 1) + hf) ^ w_swz) << 4));
+            };
+            // code reads two pairs ahead of their MFMAs
+            u32x4 wq[4];
+            wq[0] = read_w(0);
+            wq[1] = read_w(1);
+#pragma unroll
+            for (int pr = 0; pr < 4; ++pr) {
+                if (pr + 2 < 4) wq[pr + 2] = read_w(pr + 2);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const uint2 lo = e4m3x4_to_f16(wq[pr][2 * q]), hi = e4m3x4_to_f16(wq[pr][2 * q + 1]);
+                    acc = mfma32(__builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y}),
+                                 aop[8 * st + 2 * pr + q], acc);
+                }
+                if (st == 1 && pr == 1 && ci > 0) store(ci - 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        park(acc);  // the wave's staging was read back in this chunk's K stage 1
+    }
+    store(nch - 1);
 }
 
 // Per-row E4M3 quantization of an fp16 weight [rows, cols] (reference
@@ -951,6 +1203,35 @@ hipError_t launch_q_cross_attention(const LinearParams& params_in, bool w_fp8, i
     else if (w_fp8) SDXL_QX(true, false);
     else SDXL_QX(false, false);
 #undef SDXL_QX
+    return hipGetLastError();
+}
+
+bool ln_linear_supported(const LnLinearParams& p) {
+    return p.k == 640 && p.m > 0 && p.n >= 128 && p.n % 128 == 0 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+           ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 && p.ldw % 16 == 0 &&
+           ((uintptr_t)p.w & 15) == 0 && p.w_scale != nullptr && ((uintptr_t)p.w_scale & 3) == 0 &&
+           (p.bias == nullptr || ((uintptr_t)p.bias & 1) == 0) && p.ldc % 4 == 0 && ((uintptr_t)p.c & 7) == 0 &&
+           p.ldw * 128 <= 0x7FFFFFFF;  // 32-bit transfer offsets
+}
+
+hipError_t launch_ln_linear(const LnLinearParams& params_in, int compute_units, hipStream_t stream) {
+    LnLinearParams p = params_in;
+    if (!ln_linear_supported(p)) return hipErrorInvalidValue;
+    // One workgroup per CU (140 KiB of LDS): row blocks of 64, and the output
+    // columns split so that the grid fills the CUs once (at most
+    // kLnLinMaxCols columns per workgroup).
+    const int cus = compute_units > 0 ? compute_units : 256;
+    p.m_blocks = (p.m + 63) / 64;
+    p.chunks = p.n / 128;
+    const int min_split = (p.chunks * 128 + kLnLinMaxCols - 1) / kLnLinMaxCols;
+    const int fill = p.m_blocks >= cus ? 1 : cus / p.m_blocks;
+    p.n_split = std::min(p.chunks, std::max(min_split, fill));
+    const int64_t tasks = (int64_t)p.m_blocks * p.n_split;
+    if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)tasks), block(512);
+    const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;
+    if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, true>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((ln_linear_kernel<640, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 

@@ -178,6 +178,69 @@ sdxl_status linear_impl(const sdxl_linear_desc* d, const void* a, const float* a
 
 }  // namespace
 
+namespace {
+
+// Validation of sdxl_layer_norm_linear; fills p. SDXL_STATUS_UNSUPPORTED for
+// shapes the fused kernel does not take (the caller may compose instead).
+sdxl_status ln_linear_params(const sdxl_linear_desc* d, const void* x, const void* gamma, const void* beta, float eps,
+                             const void* w, const float* w_scale, const void* bias, void* c,
+                             sdxl_hip::LnLinearParams& p) {
+    if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm_linear: null descriptor");
+    if (d->reserved != 0 || d->residual_row_stride != 0)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT,
+                             "sdxl_layer_norm_linear: reserved and residual_row_stride must be 0");
+    if (d->m < 0 || d->n < 0 || d->k <= 0 || d->m > INT32_MAX || d->n > INT32_MAX || d->k > INT32_MAX)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_layer_norm_linear: dimensions out of range");
+    const int64_t ldx = d->a_row_stride ? d->a_row_stride : d->k;
+    const int64_t ldw = d->w_row_stride ? d->w_row_stride : d->k;
+    const int64_t ldc = d->c_row_stride ? d->c_row_stride : d->n;
+    if (ldx < d->k || ldw < d->k || ldc < d->n)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_SHAPE, "sdxl_layer_norm_linear: row stride smaller than the row");
+    if (d->w_dtype != SDXL_DTYPE_E4M3)
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED, "sdxl_layer_norm_linear: weights must be E4M3");
+    if (w_scale == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "FP8 weight has invalid scaling metadata");
+    if (x == nullptr || gamma == nullptr || beta == nullptr || w == nullptr || c == nullptr)
+        return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm_linear: null tensor pointer");
+    p = sdxl_hip::LnLinearParams{};
+    p.x = x;
+    p.gamma = gamma;
+    p.beta = beta;
+    p.w = static_cast<const uint8_t*>(w);
+    p.w_scale = w_scale;
+    p.bias = bias;
+    p.c = c;
+    p.ldx = ldx;
+    p.ldw = ldw;
+    p.ldc = ldc;
+    p.m = (int32_t)d->m;
+    p.n = (int32_t)d->n;
+    p.k = (int32_t)d->k;
+    p.eps = eps > 0.0f ? eps : 1.0e-5f;
+    if (d->m > 0 && d->n > 0 && !sdxl_hip::ln_linear_supported(p))
+        return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED,
+                             "sdxl_layer_norm_linear: needs k == 640, n % 128 == 0, 16-byte aligned x rows, gamma, beta "
+                             "and w rows, 8-byte aligned c rows");
+    return SDXL_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+sdxl_status sdxl_layer_norm_linear(const sdxl_linear_desc* d, const void* x, const void* gamma, const void* beta,
+                                   float eps, const void* w, const float* w_scale, const void* bias, void* c,
+                                   void* stream) {
+    sdxl_hip::LnLinearParams p;
+    const sdxl_status st = ln_linear_params(d, x, gamma, beta, eps, w, w_scale, bias, c, p);
+    if (st != SDXL_STATUS_OK) return st;
+    if (p.m == 0 || p.n == 0) return SDXL_STATUS_OK;
+    return launch_status(sdxl_hip::launch_ln_linear(p, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                         "sdxl_layer_norm_linear");
+}
+
+}  // extern "C"
+
 extern "C" {
 
 sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w, const float* w_scale,
@@ -251,9 +314,20 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
         if (st != SDXL_STATUS_OK) return st;
         st = sdxl_linear_e4m3(&qd, codes, code_scale, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
     } else {
-        st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
-        if (st != SDXL_STATUS_OK) return st;
-        st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+        // LayerNorm fused into the projection where the kernel takes the shape
+        // (E4M3 weights, width 640: the level-1 blocks); else two launches.
+        sdxl_hip::LnLinearParams lp;
+        const bool fuse = d->ln_fusion == 0 && d->w_qkv_dtype == SDXL_DTYPE_E4M3 &&
+                          ln_linear_params(&qd, x, ln_gamma, ln_beta, d->ln_eps, w_qkv, w_qkv_scale, nullptr, qkv,
+                                           lp) == SDXL_STATUS_OK;
+        if (fuse) {
+            st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                               "sdxl_attn_sublayer");
+        } else {
+            st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+            if (st != SDXL_STATUS_OK) return st;
+            st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
+        }
     }
     if (st != SDXL_STATUS_OK) return st;
 

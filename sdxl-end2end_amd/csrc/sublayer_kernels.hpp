@@ -54,6 +54,27 @@ struct LayerNormParams {
 };
 hipError_t launch_layer_norm(const LayerNormParams& params, hipStream_t stream);
 
+// LayerNorm fused with a projection on E4M3 weights (k = 640):
+// c[m, n] = w_scale[n] * sum_k LN(x)[m, k] * w[n, k] + bias[n], LN(x) rounded to
+// fp16 exactly as launch_layer_norm rounds it. Requires n % 128 == 0, 16-byte
+// aligned x rows, gamma, beta and w rows (ldw % 16 == 0), 8-byte aligned c
+// rows; strides in elements (w: bytes).
+struct LnLinearParams {
+    const void* x;
+    const void* gamma;
+    const void* beta;
+    const uint8_t* w;
+    const float* w_scale;
+    const void* bias;  // nullable
+    void* c;
+    int64_t ldx, ldw, ldc;
+    int32_t m, n, k;
+    float eps;
+    int32_t m_blocks, n_split, chunks;  // filled by the launcher
+};
+bool ln_linear_supported(const LnLinearParams& params);
+hipError_t launch_ln_linear(const LnLinearParams& params, int compute_units, hipStream_t stream);
+
 struct QuantizeParams {
     const void* w;   // fp16 [rows, cols]
     uint8_t* q;      // E4M3 [rows, cols]

@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     "sdxl_layer_norm_e4m3",
     "sdxl_linear",
     "sdxl_linear_e4m3",
+    "sdxl_layer_norm_linear",
     "sdxl_attn_sublayer_noalloc",
     "sdxl_attn_sublayer_noalloc_max_workspace_bytes",
     "sdxl_quantize_e4m3_rows",
@@ -77,7 +78,7 @@ class SublayerDesc(ctypes.Structure):
 
     _fields_ = [("batch", ctypes.c_int64), ("seq", ctypes.c_int64), ("heads", ctypes.c_int64),
                 ("w_qkv_dtype", ctypes.c_int32), ("attn_backend", ctypes.c_int32),
-                ("ln_eps", ctypes.c_float), ("qkv_activations", ctypes.c_int32)]
+                ("ln_eps", ctypes.c_float), ("qkv_activations", ctypes.c_int32), ("ln_fusion", ctypes.c_int32)]
 
 
 class CrossSublayerDesc(ctypes.Structure):
@@ -134,6 +135,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sdxl_linear.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp]
     lib.sdxl_linear_e4m3.restype = ctypes.c_int
     lib.sdxl_linear_e4m3.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.sdxl_layer_norm_linear.restype = ctypes.c_int
+    lib.sdxl_layer_norm_linear.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]
     lib.sdxl_quantize_e4m3_rows.restype = ctypes.c_int
     lib.sdxl_quantize_e4m3_rows.argtypes = [i64, i64, vp, vp, vp, vp]
     lib.sdxl_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
@@ -317,6 +320,22 @@ def linear(a, w, w_scale=None, bias=None, residual=None, out=None):
     return out
 
 
+def layer_norm_linear(x, gamma, beta, w, w_scale, bias=None, eps: float = 1e-5, out=None):
+    """LayerNorm fused into an E4M3-weight projection (sdxl_layer_norm_linear): x [M, K] fp16 (K = 640),
+    w uint8 E4M3 [N, K] with w_scale [N]; returns LN(x) . w^T * w_scale + bias as fp16 [M, N], equal to
+    linear(layer_norm(x), w, w_scale, bias)."""
+    import torch
+    M, K = x.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    d = LinearDesc(m=M, n=N, k=K, a_row_stride=x.stride(0), w_row_stride=w.stride(0), c_row_stride=out.stride(0),
+                   residual_row_stride=0, w_dtype=E4M3, reserved=0)
+    _check(load().sdxl_layer_norm_linear(ctypes.byref(d), _ptr(x), _ptr(gamma), _ptr(beta), eps, _ptr(w),
+                                         _ptr(w_scale), _ptr(bias), _ptr(out), _stream(x)))
+    return out
+
+
 def quantize_e4m3_rows(w):
     """Per-output-channel E4M3 weight quantisation (reference src/cuda/weights.cu:119-170):
     returns (codes uint8 [N, K], scales fp32 [N])."""
@@ -334,7 +353,8 @@ def sublayer_workspace_bytes(batch: int, seq: int, heads: int) -> int:
 
 
 def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads: int, out=None,
-                  workspace=None, backend: int = AUTO, eps: float = 0.0, fp8_activations: bool = False):
+                  workspace=None, backend: int = AUTO, eps: float = 0.0, fp8_activations: bool = False,
+                  ln_fusion: bool = True):
     """x + to_out(attention(LN(x) . w_qkv^T)) for hidden x [B, S, W] fp16 (reference
     src/cuda/unet.cpp:106-118 with q/k/v fused): w_qkv [3W, W] fp16 or uint8 E4M3 + w_qkv_scale [3W].
     fp8_activations: LayerNorm emits E4M3 codes and the QKV projection runs on fp8 MFMA."""
@@ -343,7 +363,8 @@ def attn_sublayer(x, ln_gamma, ln_beta, w_qkv, w_qkv_scale, w_out, b_out, heads:
     if out is None:
         out = torch.empty_like(x)
     d = SublayerDesc(batch=B, seq=S, heads=heads, w_qkv_dtype=E4M3 if w_qkv.dtype == torch.uint8 else F16,
-                     attn_backend=backend, ln_eps=eps, qkv_activations=E4M3 if fp8_activations else F16)
+                     attn_backend=backend, ln_eps=eps, qkv_activations=E4M3 if fp8_activations else F16,
+                     ln_fusion=0 if ln_fusion else 1)
     nbytes = int(load().sdxl_attn_sublayer_workspace_bytes(ctypes.byref(d)))
     if workspace is None:
         workspace = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=x.device)

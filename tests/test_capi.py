@@ -2,6 +2,7 @@
 function include/sdxl_hip/attention.h and sublayer.h declare, and reproduces the reference's
 backend spellings, eligibility rules and error behaviour
 (src/cuda/runtime.cpp:61-87, src/cuda/ops_kernels.cu:1912-1952)."""
+import ctypes
 import os
 import re
 import subprocess
@@ -30,7 +31,7 @@ def test_header_declarations_are_exported():
     lib = sh.load()
     for n in names:
         assert hasattr(lib, n)
-    assert lib.sdxl_abi_version() == 1
+    assert lib.sdxl_abi_version() == 2
 
 
 @pytest.mark.parametrize("name,value", [
@@ -216,3 +217,22 @@ def test_cross_sublayer_workspace_and_validation():
         sh.INVALID_ARGUMENT
     d = sh.CrossSublayerDesc(batch=0, seq=64, heads=2, ctx_len=77)
     assert L.sdxl_cross_attn_sublayer(ctypes.byref(d), *args, 0, 16, 16, 16, None, 0, None) == sh.OK  # empty
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(k=1280), sh.UNSUPPORTED),          # only width 640 is fused
+    (dict(n=192), sh.UNSUPPORTED),           # n % 128 != 0
+    (dict(w_dtype=sh.F16), sh.UNSUPPORTED),  # E4M3 weights only
+    (dict(residual_row_stride=640), sh.INVALID_ARGUMENT),
+    (dict(a_row_stride=320), sh.INVALID_SHAPE),
+])
+def test_layer_norm_linear_validation(kw, status):
+    """sdxl_layer_norm_linear refuses what its kernel does not take, before touching the device
+    (placeholder pointers are never dereferenced)."""
+    fields = dict(m=64, n=1920, k=640, a_row_stride=0, w_row_stride=0, c_row_stride=0, residual_row_stride=0,
+                  w_dtype=sh.E4M3, reserved=0)
+    fields.update(kw)
+    d = sh.LinearDesc(**fields)
+    p = 1 << 20
+    st = sh.load().sdxl_layer_norm_linear(ctypes.byref(d), p, p, p, 0.0, p, p, None, p, None)
+    assert st == status

@@ -158,6 +158,67 @@ def test_linear_strided_in_place_residual():
     within_half_ulp(host(y), ref, 1e-4, "linear in place")
 
 
+# ---------------------------------------------------------------- LayerNorm fused into the projection
+
+@pytest.mark.parametrize("M,N,bias,strided", [(8192, 1920, False, False), (8100, 1920, True, False),
+                                              (200, 640, True, True), (1, 128, False, False),
+                                              (4096, 128, False, True), (130, 3840, True, False),
+                                              (1000, 1920, False, False)])
+def test_layer_norm_linear(M, N, bias, strided):
+    """sdxl_layer_norm_linear (norm1 -> q|k|v at width 640) equals sdxl_layer_norm followed by
+    sdxl_linear bit for bit (same LayerNorm rounding, same fp32 sums), and the oracle's fp32
+    LayerNorm, rounded to fp16 as the reference stores it, then linear on the dequantised
+    weights, within the linear bar. Non-trivial gamma/beta; ragged row blocks (8100, 200, 130,
+    1); one- and several-chunk column ranges, uneven splits (1000 rows: 15 chunks over 16
+    workgroups of a row block is capped at one chunk each; 130 x 3840: 30 chunks, two
+    workgroups of at most 2048 columns); strided x and c."""
+    K = 640
+    print(f"ln_linear M{M} N{N} bias{bias} strided{strided}", flush=True)
+    xb = oracle.normal_f16(1100 + M, (M, K))
+    gb = oracle.normal_f16(1101, (K,), 0.5)
+    bb = oracle.normal_f16(1102, (K,), 0.5)
+    q, s = oracle.quantize_e4m3_rows(oracle.normal_f32(1103 + N, (N, K), 0.02))
+    biasb = oracle.normal_f16(1104, (N,), 0.02) if bias else None
+    if strided:
+        x = dev16(np.concatenate([xb, oracle.normal_f16(1105, (M, 128))], axis=1))[:, :K]
+        out_base = torch.zeros((M, N + 64), dtype=torch.float16, device=DEV)
+        out = out_base[:, :N]
+    else:
+        x, out = dev16(xb), None
+    g, b = dev16(gb), dev16(bb)
+    wq, ws = torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV)
+    bias_t = dev16(biasb) if bias else None
+    got = sh.layer_norm_linear(x, g, b, wq, ws, bias=bias_t, out=out)
+    comp = sh.linear(sh.layer_norm(x, g, b), wq, w_scale=ws, bias=bias_t)
+    torch.cuda.synchronize()
+    assert torch.equal(got, comp)
+    if strided:
+        assert torch.count_nonzero(out_base[:, N:]) == 0
+    rows = np.r_[0:64, M // 2:M // 2 + 32, M - 70:M] if M > 256 else np.arange(M)
+    n32 = oracle.layer_norm(oracle.f16_bits_to_f32(xb[rows]), oracle.f16_bits_to_f32(gb), oracle.f16_bits_to_f32(bb))
+    wdq = oracle.dequantize_e4m3_rows(q, s)
+    ref = _linear_ref(f16(n32), wdq, biasb)
+    # the LayerNorm output may sit one fp16 rounding away from the oracle's (half an ulp
+    # each, pinned by test_layer_norm); its worst-case effect on each sum is added to the bar
+    ln_term = (np.abs(n32).astype(np.float64) * 2.0 ** -11) @ np.abs(wdq.astype(np.float64)).T
+    err = np.abs(host(got)[rows].astype(np.float64) - ref)
+    bound = np.abs(ref) * 2.0 ** -10 + 1e-4 + ln_term
+    print(f"LN+linear {M}x{N}: max_abs={err.max():.3e} worst_margin={np.max(err - bound):.3e}", flush=True)
+    assert (err <= bound).all(), float(err.max())
+
+
+def test_sublayer_layer_norm_fusion_switch():
+    """configs[3] sublayer with the LayerNorm inside the q|k|v projection (default) and as its own
+    launch (ln_fusion off): the same bits."""
+    x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(2, 4096, 10, 1110)
+    gamma = dev16(oracle.normal_f16(1111, (640,), 0.5))
+    beta = dev16(oracle.normal_f16(1112, (640,), 0.5))
+    y1 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10)
+    y2 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, ln_fusion=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
 # ---------------------------------------------------------------- sublayer (configs[3])
 
 def _sublayer_inputs(B, S, H, seed):
