@@ -1036,7 +1036,12 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
                     acc = mfma32(__builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y}),
                                  aop[8 * st + 2 * pr + q], acc);
                 }
-                if (st == 1 && pr == 1 && ci > 0) store(ci - 1);
+                if (st == 1 && pr == 1 && ci > 0) {
+                    store(ci - 1);
+                    // the stores stay here, ahead of the next stage's wait,
+                    // which counts them (a compiler barrier only)
+                    asm volatile("" ::: "memory");
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
