@@ -757,6 +757,75 @@ __device__ __forceinline__ f16x8v ln_out_v8(const float* v, float mean, float in
     return o;
 }
 
+// Sum over each 16-lane row of the wave (DPP butterfly: quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror); every lane of a row ends with the
+// same value (each step adds two partial sums, commutatively).
+__device__ __forceinline__ float row16_sum(float x) {
+    x = dpp_pair_add<0xB1>(x);
+    x = dpp_pair_add<0x4E>(x);
+    x = dpp_pair_add<0x141>(x);
+    x = dpp_pair_add<0x140>(x);
+    return x;
+}
+
+// LayerNorm of four rows per wave for widths that are a multiple of 128: lane
+// l works on row l / 16 and holds its 16-byte chunks l % 16 + 16 i (i <
+// kCpl = width / 128), so every lane is busy and a row's sums need no
+// cross-row exchange. Two-pass centred variance, every operation rounded on
+// its own (as ln_row_stats_v8). Writes the normalised chunks through put(i,
+// chunk index, value).
+template <int kCpl, typename Put>
+__device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl], const f16x8v (&bb)[kCpl],
+                                         float eps, Put&& put) {
+#pragma clang fp contract(off)
+    constexpr int kWidth = 128 * kCpl;
+    float v[8 * kCpl];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[8 * i + e] = (float)h[i][e];
+            sum += v[8 * i + e];
+        }
+    const float mean = row16_sum(sum) / (float)kWidth;
+    float sq = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8 * kCpl; ++k) {
+        const float d = v[k] - mean;
+        sq += d * d;
+    }
+    const float var = fmaxf(row16_sum(sq) / (float)kWidth, 0.0f);
+    const float inv = 1.0f / sqrtf(var + eps);
+    const int j = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i) put(i, j + 16 * i, ln_out_v8(v + 8 * i, mean, inv, gg[i], bb[i]));
+}
+
+// fp16 LayerNorm for widths 128 kCpl: 16 rows per 256-thread block, four per
+// wave (ln_rows4).
+template <int kCpl, bool kNt>
+__global__ __launch_bounds__(256) void layer_norm_r4_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t r = row < p.rows ? row : p.rows - 1;  // rows past the end repeat the last (not stored)
+    const int j = lane & 15;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + r * p.ldx);
+    const f16x8v* g = (const f16x8v*)p.gamma;
+    const f16x8v* bt = (const f16x8v*)p.beta;
+    f16x8v h[kCpl], gg[kCpl], bb[kCpl];
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i) {
+        h[i] = x[j + 16 * i];
+        gg[i] = g[j + 16 * i];
+        bb[i] = bt[j + 16 * i];
+    }
+    f16x8v* y = (f16x8v*)((_Float16*)p.y + r * p.ldy);
+    ln_rows4<kCpl>(h, gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
+        if (row < p.rows) store_out<kNt>(o, y + c);
+    });
+}
+
 template <int kChunks, bool kNt, bool kE4M3>
 __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
@@ -851,7 +920,6 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     constexpr int kStageBytes = 2 * 128 * 64;  // two sub-stages of 128 code rows x 64 bytes
     constexpr int kRing = 3;
     constexpr int kARow = 2 * kK;            // one normalised row, bytes
-    constexpr int kLnChunks = (kK / 8 + 63) / 64;
     static_assert(kK % 128 == 0, "128-column K stages; the operand swizzle works on groups of 16 chunks");
     static_assert(8 * 32 * 128 <= 64 * kARow, "epilogue staging fits in the row buffer");
     __shared__ __attribute__((aligned(16))) char ring[kRing][kStageBytes];
@@ -907,39 +975,33 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
         }
     }
 
-    // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7; rows past
-    // m repeat row m - 1). Row r's 16-byte chunk c sits at slot c ^ (r & 15).
+    // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7 as two groups
+    // of four, ln_rows4: the standalone LayerNorm's arithmetic; rows past m
+    // repeat row m - 1). Row r's 16-byte chunk c sits at slot c ^ (r & 15).
     {
-        constexpr int kChunks = kK / 8;
+        constexpr int kCpl = kK / 128;
+        const int j = lane & 15;
         const f16x8v* g = (const f16x8v*)p.gamma;
         const f16x8v* bt = (const f16x8v*)p.beta;
-        f16x8v gg[kLnChunks], bb[kLnChunks];
+        f16x8v gg[kCpl], bb[kCpl], h[2][kCpl];
 #pragma unroll
-        for (int j = 0; j < kLnChunks; ++j) {
-            gg[j] = g[min(lane + 64 * j, kChunks - 1)];
-            bb[j] = bt[min(lane + 64 * j, kChunks - 1)];
+        for (int i = 0; i < kCpl; ++i) {
+            gg[i] = g[j + 16 * i];
+            bb[i] = bt[j + 16 * i];
         }
-        f16x8v h[8][kLnChunks];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int gm = min(m0 + 8 * wave + i, p.m - 1);
+        for (int half = 0; half < 2; ++half) {
+            const int gm = min(m0 + 8 * wave + 4 * half + (lane >> 4), p.m - 1);
             const f16x8v* xr = (const f16x8v*)((const _Float16*)p.x + (int64_t)gm * p.ldx);
 #pragma unroll
-            for (int j = 0; j < kLnChunks; ++j) h[i][j] = xr[min(lane + 64 * j, kChunks - 1)];
+            for (int i = 0; i < kCpl; ++i) h[half][i] = xr[j + 16 * i];
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 8 * wave + i;
-            float v[8 * kLnChunks];
-            float mean, inv;
-            ln_row_stats_v8<kLnChunks>(h[i], lane, kChunks, kK, p.eps, v, mean, inv);
-#pragma unroll
-            for (int j = 0; j < kLnChunks; ++j) {
-                const int c = lane + 64 * j;
-                if (c < kChunks)
-                    *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) =
-                        ln_out_v8(v + 8 * j, mean, inv, gg[j], bb[j]);
-            }
+        for (int half = 0; half < 2; ++half) {
+            const int r = 8 * wave + 4 * half + (lane >> 4);
+            ln_rows4<kCpl>(h[half], gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
+                *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) = o;
+            });
         }
     }
     __syncthreads();
@@ -1253,6 +1315,27 @@ hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t strea
     // [1024, 2048] 4.5 -> 4.1 us, but width 640 (80 chunks: a quarter of the
     // lanes take two) 7.3 -> 7.6 us, so E4M3 rows narrower than 1024 keep the
     // pair kernel.
+    // Four rows per wave (the form the fused LayerNorm projection shares) for
+    // fp16 output at widths 128 .. 640 in steps of 128: configs[3]'s [8192, 640]
+    // 5.65 -> 4.45 us (every lane busy: 80 chunks over 64 lanes left three
+    // quarters of them idle in the second pass); at width 1280 (160 VGPRs,
+    // occupancy 3) it measured 4.7 against 4.1-4.3 us, so wider rows keep the
+    // 16-byte kernel below.
+    if (!e4m3 && p.width % 128 == 0 && p.width <= 640 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+        ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 && p.ldy % 8 == 0 &&
+        ((uintptr_t)p.y & 15) == 0) {
+        const dim3 g16((unsigned)((p.rows + 15) / 16));
+        switch (p.width / 128) {
+#define SDXL_LNR4(n)                                                                            \
+    case n:                                                                                     \
+        if (nt) hipLaunchKernelGGL((layer_norm_r4_kernel<n, true>), g16, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((layer_norm_r4_kernel<n, false>), g16, block, 0, stream, p);    \
+        break;
+            SDXL_LNR4(1) SDXL_LNR4(2) SDXL_LNR4(3) SDXL_LNR4(4) SDXL_LNR4(5)
+#undef SDXL_LNR4
+        }
+        return hipGetLastError();
+    }
     const bool v8 = p.width % 8 == 0 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
                     ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 &&
                     (e4m3 ? p.width >= 1024 && p.ldy % 8 == 0 && ((uintptr_t)p.y & 7) == 0
