@@ -214,6 +214,17 @@ def bench_sublayer(torch, sh, steps=50, warmup=5, B=2, S=4096, H=10):
             e["tflops"] = round(fl / (t * 1e-3) / 1e12, 1)
             e["fp8_mfma_frac"] = round(fl / (t * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)
         out["fp8_activations"][name] = e
+    if W == 640:
+        # E4M3 LayerNorm inside the fp8 projection (sdxl_layer_norm_linear_e4m3): replaces the two stages above
+        fl, by = sh.linear_flops(M, 3 * W, W), 2.0 * M * W + 3 * W * W + 2.0 * M * 3 * W
+        t = time_fn(torch, lambda: sh.layer_norm_linear(x.view(M, W), gamma, beta, q8, s8, out=qkv,
+                                                        fp8_activations=True), steps, warmup)
+        out["fp8_activations"]["layer_norm_e4m3_qkv_fused"] = {
+            "us": round(t * 1e3, 2), "tflops": round(fl / (t * 1e-3) / 1e12, 1),
+            "fp8_mfma_frac": round(fl / (t * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)}
+        t = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws,
+                                                    fp8_activations=True, ln_fusion=False), steps, warmup)
+        out["fp8_activations"]["fused_call_separate_ln_us"] = round(t * 1e3, 2)
     t = time_fn(torch, lambda: sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y, workspace=ws,
                                                 fp8_activations=True), steps, warmup)
     out["fp8_activations"]["fused_call_us"] = round(t * 1e3, 2)

@@ -99,6 +99,16 @@ sdxl_status sdxl_layer_norm_linear(const sdxl_linear_desc* desc, const void* x, 
                                    const void* beta, float eps, const void* w, const float* w_scale,
                                    const void* bias, void* c, void* stream);
 
+/* sdxl_layer_norm_linear with FP8 activations on the fp8 matrix cores: the LayerNorm rounds each
+ * normalised row to E4M3 codes with its per-row scale exactly as sdxl_layer_norm_e4m3 does, and
+ * c = codes . w^T * row_scale * w_scale (+ bias), the same bits as sdxl_layer_norm_e4m3 followed by
+ * sdxl_linear_e4m3; neither the codes nor the scales reach HBM. No counterpart in the reference
+ * (weight-only FP8 there): the fused form of the optional fp8 QKV projection. Same arguments and
+ * shape rules as sdxl_layer_norm_linear. */
+sdxl_status sdxl_layer_norm_linear_e4m3(const sdxl_linear_desc* desc, const void* x, const void* gamma,
+                                        const void* beta, float eps, const void* w, const float* w_scale,
+                                        const void* bias, void* c, void* stream);
+
 typedef struct sdxl_sublayer_desc {
     int64_t batch;
     int64_t seq;
@@ -111,9 +121,10 @@ typedef struct sdxl_sublayer_desc {
      * output per row and the projection runs on the fp8 matrix cores; needs E4M3
      * w_qkv). */
     int32_t qkv_activations;
-    /* 0: the LayerNorm runs inside the q|k|v projection (sdxl_layer_norm_linear)
-     * where that kernel takes the shape (fp16 activations, E4M3 w_qkv, width 640),
-     * else as its own launch; 1: always its own launch. Same results either way. */
+    /* 0: the LayerNorm runs inside the q|k|v projection (sdxl_layer_norm_linear, or
+     * sdxl_layer_norm_linear_e4m3 with E4M3 activations) where that kernel takes the
+     * shape (E4M3 w_qkv, width 640), else as its own launch; 1: always its own
+     * launch. Same results either way. */
     int32_t ln_fusion;
 } sdxl_sublayer_desc;
 

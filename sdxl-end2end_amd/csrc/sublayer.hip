@@ -768,18 +768,30 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-// LayerNorm of four rows per wave for widths that are a multiple of 128: lane
-// l works on row l / 16 and holds its 16-byte chunks l % 16 + 16 i (i <
-// kCpl = width / 128), so every lane is busy and a row's sums need no
-// cross-row exchange. Two-pass centred variance, every operation rounded on
-// its own (as ln_row_stats_v8). Writes the normalised chunks through put(i,
-// chunk index, value).
-template <int kCpl, typename Put>
-__device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl], const f16x8v (&bb)[kCpl],
-                                         float eps, Put&& put) {
+// Maximum over each 16-lane row of the wave (the same DPP pattern as row16_sum).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_pair_max(float x) {
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xF, 0xF, false);
+    return fmaxf(x, __builtin_bit_cast(float, moved));
+}
+__device__ __forceinline__ float row16_max(float x) {
+    x = dpp_pair_max<0xB1>(x);
+    x = dpp_pair_max<0x4E>(x);
+    x = dpp_pair_max<0x141>(x);
+    x = dpp_pair_max<0x140>(x);
+    return x;
+}
+
+// LayerNorm statistics of four rows per wave for widths that are a multiple of
+// 128: lane l works on row l / 16 and holds its 16-byte chunks l % 16 + 16 i
+// (i < kCpl = width / 128), so every lane is busy and a row's sums need no
+// cross-row exchange. Two-pass centred variance, every operation rounded on its
+// own (as ln_row_stats_v8). v receives the row's values in fp32.
+template <int kCpl>
+__device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float eps, float (&v)[8 * kCpl], float& mean,
+                                               float& inv) {
 #pragma clang fp contract(off)
     constexpr int kWidth = 128 * kCpl;
-    float v[8 * kCpl];
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
@@ -788,7 +800,7 @@ __device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (
             v[8 * i + e] = (float)h[i][e];
             sum += v[8 * i + e];
         }
-    const float mean = row16_sum(sum) / (float)kWidth;
+    mean = row16_sum(sum) / (float)kWidth;
     float sq = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8 * kCpl; ++k) {
@@ -796,10 +808,63 @@ __device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (
         sq += d * d;
     }
     const float var = fmaxf(row16_sum(sq) / (float)kWidth, 0.0f);
-    const float inv = 1.0f / sqrtf(var + eps);
+    inv = 1.0f / sqrtf(var + eps);
+}
+
+// fp16 LayerNorm of four rows per wave (ln_rows4_stats); writes the normalised
+// chunks through put(i, chunk index, value).
+template <int kCpl, typename Put>
+__device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl], const f16x8v (&bb)[kCpl],
+                                         float eps, Put&& put) {
+    float v[8 * kCpl];
+    float mean, inv;
+    ln_rows4_stats<kCpl>(h, eps, v, mean, inv);
     const int j = threadIdx.x & 15;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i) put(i, j + 16 * i, ln_out_v8(v + 8 * i, mean, inv, gg[i], bb[i]));
+}
+
+// E4M3 codes of four values y / scale (r = 1 / scale, correctly rounded): the
+// quotient from the reciprocal plus one Markstein correction (the correctly
+// rounded quotient), saturated to +-448, rounded to nearest even.
+__device__ __forceinline__ uint32_t e4m3_code4(const float* y4, float scale, float r) {
+    float q[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float q0 = y4[e] * r;
+        q[e] = fminf(fmaxf(__builtin_fmaf(__builtin_fmaf(-q0, scale, y4[e]), r, q0), -448.0f), 448.0f);
+    }
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[0], q[1], 0u, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
+}
+
+// E4M3 LayerNorm of four rows per wave: the normalised fp32 row (ln_affine),
+// its scale max(amax / 448, 1e-12) (1 for an all-zero row) and the codes
+// E4M3(y / scale) (the weight quantiser's rule). put(i, chunk index, 8 codes as
+// two dwords); returns the row's scale (the same in all 16 lanes of the row).
+template <int kCpl, typename Put>
+__device__ __forceinline__ float ln_rows4_e4m3(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl],
+                                               const f16x8v (&bb)[kCpl], float eps, Put&& put) {
+#pragma clang fp contract(off)
+    float v[8 * kCpl];
+    float mean, inv;
+    ln_rows4_stats<kCpl>(h, eps, v, mean, inv);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[8 * i + e] = ln_affine(v[8 * i + e], mean, inv, gg[i][e], bb[i][e]);
+            amax = fmaxf(amax, fabsf(v[8 * i + e]));
+        }
+    amax = row16_max(amax);
+    const float scale = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
+    const float r = 1.0f / scale;
+    const int j = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+        put(i, j + 16 * i, u32x2{e4m3_code4(v + 8 * i, scale, r), e4m3_code4(v + 8 * i + 4, scale, r)});
+    return scale;
 }
 
 // fp16 LayerNorm for widths 128 kCpl: 16 rows per 256-thread block, four per
@@ -824,6 +889,31 @@ __global__ __launch_bounds__(256) void layer_norm_r4_kernel(LayerNormParams p) {
     ln_rows4<kCpl>(h, gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
         if (row < p.rows) store_out<kNt>(o, y + c);
     });
+}
+
+// E4M3 LayerNorm (codes + per-row scales) for widths 128 kCpl, four rows per
+// wave (ln_rows4_e4m3).
+template <int kCpl, bool kNt>
+__global__ __launch_bounds__(256) void layer_norm_r4_e4m3_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const int64_t r = row < p.rows ? row : p.rows - 1;  // rows past the end repeat the last (not stored)
+    const int j = lane & 15;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + r * p.ldx);
+    const f16x8v* g = (const f16x8v*)p.gamma;
+    const f16x8v* bt = (const f16x8v*)p.beta;
+    f16x8v h[kCpl], gg[kCpl], bb[kCpl];
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i) {
+        h[i] = x[j + 16 * i];
+        gg[i] = g[j + 16 * i];
+        bb[i] = bt[j + 16 * i];
+    }
+    u32x2* y = (u32x2*)((uint8_t*)p.y + r * p.ldy);
+    const float scale = ln_rows4_e4m3<kCpl>(h, gg, bb, p.eps, [&](int, int c, u32x2 codes) __attribute__((always_inline)) {
+        if (row < p.rows) store_out<kNt>(codes, y + c);
+    });
+    if (row < p.rows && j == 0) p.y_scale[row] = scale;
 }
 
 template <int kChunks, bool kNt, bool kE4M3>
@@ -913,19 +1003,20 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
 // wait counts exactly the transfers it needs.
 constexpr int kLnLinMaxCols = 2048;  // output columns per workgroup (scales and bias in LDS)
 
-template <int kK, bool kNt>
+template <int kK, bool kAFp8, bool kNt>
 __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     constexpr int kStages = kK / 128;        // 128-column K stages per chunk
     constexpr int kSteps = kK / 16;          // MFMA K steps
     constexpr int kStageBytes = 2 * 128 * 64;  // two sub-stages of 128 code rows x 64 bytes
     constexpr int kRing = 3;
-    constexpr int kARow = 2 * kK;            // one normalised row, bytes
+    constexpr int kARow = kAFp8 ? kK : 2 * kK;  // one normalised row, bytes (fp16 or E4M3 codes)
     static_assert(kK % 128 == 0, "128-column K stages; the operand swizzle works on groups of 16 chunks");
     static_assert(8 * 32 * 128 <= 64 * kARow, "epilogue staging fits in the row buffer");
     __shared__ __attribute__((aligned(16))) char ring[kRing][kStageBytes];
     __shared__ __attribute__((aligned(16))) char abuf[64 * kARow];
     __shared__ __attribute__((aligned(16))) float sc_lds[kLnLinMaxCols];
     __shared__ __attribute__((aligned(16))) float bias_lds[kLnLinMaxCols];
+    __shared__ float rs_lds[64];  // E4M3 activations: the rows' scales
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -999,21 +1090,44 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const int r = 8 * wave + 4 * half + (lane >> 4);
-            ln_rows4<kCpl>(h[half], gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
-                *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) = o;
-            });
+            if constexpr (kAFp8) {
+                // E4M3 rows (ln_rows4_e4m3, the standalone E4M3 LayerNorm's code):
+                // the 8 codes of fp16 chunk c at byte 8c, 16-byte slots swizzled
+                // by r & 7
+                const float sc = ln_rows4_e4m3<kCpl>(h[half], gg, bb, p.eps,
+                                                     [&](int, int c, u32x2 codes) __attribute__((always_inline)) {
+                    *(lds_u32x2*)(abuf + r * kARow + (((c >> 1) ^ (r & 7)) << 4) + 8 * (c & 1)) = codes;
+                });
+                if ((lane & 15) == 0) rs_lds[r] = sc;
+            } else {
+                ln_rows4<kCpl>(h[half], gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
+                    *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) = o;
+                });
+            }
         }
     }
     __syncthreads();
     // Activation operands of the wave's rows: step ks = 4 s + 2 pp + q (s: 64-column
     // sub-stage) takes columns 64 s + 32 pp + 16 hf + 8 q .. +7 (linear_kernel's K order).
-    i16x8 aop[kSteps];
+    // E4M3 activations: one fp8 MFMA per 64-column sub-stage s, the lane
+    // supplying bytes 64 s + 32 hf .. +31 of its row (linear_kernel's fp8 order).
+    i16x8 aop[kAFp8 ? 1 : kSteps];
+    i32x8 aop8[kAFp8 ? kK / 64 : 1];
     {
         const int ar = 32 * wm + col;
+        if constexpr (kAFp8) {
 #pragma unroll
-        for (int ks = 0; ks < kSteps; ++ks) {
-            const int c = 8 * (ks >> 2) + 4 * ((ks >> 1) & 1) + 2 * hf + (ks & 1);
-            aop[ks] = *(const lds_i16x8*)(abuf + ar * kARow + ((c ^ (ar & 15)) << 4));
+            for (int s8 = 0; s8 < kK / 64; ++s8) {
+                const u32x4 lo = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf) ^ (ar & 7)) << 4));
+                const u32x4 hi = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf + 1) ^ (ar & 7)) << 4));
+                aop8[s8] = __builtin_bit_cast(i32x8, u32x4x2{lo, hi});
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < kSteps; ++ks) {
+                const int c = 8 * (ks >> 2) + 4 * ((ks >> 1) & 1) + 2 * hf + (ks & 1);
+                aop[ks] = *(const lds_i16x8*)(abuf + ar * kARow + ((c ^ (ar & 15)) << 4));
+            }
         }
     }
     __syncthreads();  // the row buffer becomes the epilogue staging
@@ -1044,10 +1158,14 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
         for (int it = 0; it < 4; ++it) {
             const int r = (lane >> 3) + 8 * it;
             const int m = min(m0 + 32 * wm + r, p.m - 1);
-            const f32x4 v = *(const lds_f32x4*)(stg + r * 128 + (((lane & 7) ^ (r & 7)) << 4));
-            // fp32 value first (one fused multiply-add), then fp16, as
-            // linear_kernel's epilogue rounds: the empty asm keeps the compiler
-            // from rounding the fma straight to fp16 (v_fma_mix) in one step
+            f32x4 v = *(const lds_f32x4*)(stg + r * 128 + (((lane & 7) ^ (r & 7)) << 4));
+            if constexpr (kAFp8) {
+                const float rs = rs_lds[32 * wm + r];
+                v = f32x4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
+            }
+            // fp32 value first ((sum x row scale) then one fused multiply-add),
+            // then fp16, as linear_kernel's epilogue rounds: the empty asm keeps
+            // the compiler from rounding the fma straight to fp16 (v_fma_mix)
             f32x4 o = {__builtin_fmaf(v[0], e_scale[0], e_bias[0]), __builtin_fmaf(v[1], e_scale[1], e_bias[1]),
                        __builtin_fmaf(v[2], e_scale[2], e_bias[2]), __builtin_fmaf(v[3], e_scale[3], e_bias[3])};
             asm volatile("" : "+v"(o));
@@ -1081,9 +1199,29 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
             __syncthreads();  // stage g landed for every wave; stage g - 1's buffer is free
             if (g + 2 < G) issue_stage(g + 2);
             const char* cur = ring[g % kRing];
+            // fp16 activations: pair pr = (sub-stage pr / 2, K pair pr % 2), the
+            // lane's 16 codes of two K steps; E4M3 activations: pr = (sub-stage pr
+            // / 2, half pr % 2) of the lane's 32 code bytes 32 hf .. +31
             auto read_w = [&](int pr) __attribute__((always_inline)) {
-                return *(const lds_u32x4*)(cur + (pr >> 1) * 8192 + w_off + (((2 * (pr & 1) + hf) ^ w_swz) << 4));
+                const int chunk = kAFp8 ? 2 * hf + (pr & 1) : 2 * (pr & 1) + hf;
+                return *(const lds_u32x4*)(cur + (pr >> 1) * 8192 + w_off + ((chunk ^ w_swz) << 4));
             };
+            if constexpr (kAFp8) {
+                // both sub-stages' 32 code bytes per lane, then one fp8 MFMA each
+                u32x4 wq[4];
+#pragma unroll
+                for (int pr = 0; pr < 4; ++pr) wq[pr] = read_w(pr);
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) {
+                    acc = mfma32_fp8(__builtin_bit_cast(i32x8, u32x4x2{wq[2 * sub], wq[2 * sub + 1]}),
+                                     aop8[2 * st + sub], acc);
+                    if (st == 1 && sub == 0 && ci > 0) {
+                        store(ci - 1);
+                        asm volatile("" ::: "memory");  // as below
+                    }
+                }
+                continue;
+            }
             // code reads two pairs ahead of their MFMAs
             u32x4 wq[4];
             wq[0] = read_w(0);
@@ -1297,8 +1435,13 @@ hipError_t launch_ln_linear(const LnLinearParams& params_in, int compute_units, 
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(512);
     const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;
-    if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, true>), grid, block, 0, stream, p);
-    else hipLaunchKernelGGL((ln_linear_kernel<640, false>), grid, block, 0, stream, p);
+    if (p.a_fp8) {
+        if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, true, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ln_linear_kernel<640, true, false>), grid, block, 0, stream, p);
+    } else {
+        if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, false, true>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((ln_linear_kernel<640, false, false>), grid, block, 0, stream, p);
+    }
     return hipGetLastError();
 }
 
@@ -1333,6 +1476,23 @@ hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t strea
         break;
             SDXL_LNR4(1) SDXL_LNR4(2) SDXL_LNR4(3) SDXL_LNR4(4) SDXL_LNR4(5)
 #undef SDXL_LNR4
+        }
+        return hipGetLastError();
+    }
+    // E4M3 rows of widths 128 .. 640 in the same four-rows-per-wave form (the
+    // fused E4M3 LayerNorm projection shares its code).
+    if (e4m3 && p.width % 128 == 0 && p.width <= 640 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+        ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 && p.ldy % 8 == 0 &&
+        ((uintptr_t)p.y & 7) == 0) {
+        const dim3 g16((unsigned)((p.rows + 15) / 16));
+        switch (p.width / 128) {
+#define SDXL_LNR4E(n)                                                                                \
+    case n:                                                                                          \
+        if (nt) hipLaunchKernelGGL((layer_norm_r4_e4m3_kernel<n, true>), g16, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((layer_norm_r4_e4m3_kernel<n, false>), g16, block, 0, stream, p);    \
+        break;
+            SDXL_LNR4E(1) SDXL_LNR4E(2) SDXL_LNR4E(3) SDXL_LNR4E(4) SDXL_LNR4E(5)
+#undef SDXL_LNR4E
         }
         return hipGetLastError();
     }

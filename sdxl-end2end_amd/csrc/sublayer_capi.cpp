@@ -183,7 +183,7 @@ namespace {
 // Validation of sdxl_layer_norm_linear; fills p. SDXL_STATUS_UNSUPPORTED for
 // shapes the fused kernel does not take (the caller may compose instead).
 sdxl_status ln_linear_params(const sdxl_linear_desc* d, const void* x, const void* gamma, const void* beta, float eps,
-                             const void* w, const float* w_scale, const void* bias, void* c,
+                             const void* w, const float* w_scale, const void* bias, void* c, bool a_fp8,
                              sdxl_hip::LnLinearParams& p) {
     if (d == nullptr) return sdxl_hip_fail(SDXL_STATUS_INVALID_ARGUMENT, "sdxl_layer_norm_linear: null descriptor");
     if (d->reserved != 0 || d->residual_row_stride != 0)
@@ -217,6 +217,7 @@ sdxl_status ln_linear_params(const sdxl_linear_desc* d, const void* x, const voi
     p.n = (int32_t)d->n;
     p.k = (int32_t)d->k;
     p.eps = eps > 0.0f ? eps : 1.0e-5f;
+    p.a_fp8 = a_fp8 ? 1 : 0;
     if (d->m > 0 && d->n > 0 && !sdxl_hip::ln_linear_supported(p))
         return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED,
                              "sdxl_layer_norm_linear: needs k == 640, n % 128 == 0, 16-byte aligned x rows, gamma, beta "
@@ -232,11 +233,22 @@ sdxl_status sdxl_layer_norm_linear(const sdxl_linear_desc* d, const void* x, con
                                    float eps, const void* w, const float* w_scale, const void* bias, void* c,
                                    void* stream) {
     sdxl_hip::LnLinearParams p;
-    const sdxl_status st = ln_linear_params(d, x, gamma, beta, eps, w, w_scale, bias, c, p);
+    const sdxl_status st = ln_linear_params(d, x, gamma, beta, eps, w, w_scale, bias, c, false, p);
     if (st != SDXL_STATUS_OK) return st;
     if (p.m == 0 || p.n == 0) return SDXL_STATUS_OK;
     return launch_status(sdxl_hip::launch_ln_linear(p, compute_units(), reinterpret_cast<hipStream_t>(stream)),
                          "sdxl_layer_norm_linear");
+}
+
+sdxl_status sdxl_layer_norm_linear_e4m3(const sdxl_linear_desc* d, const void* x, const void* gamma, const void* beta,
+                                        float eps, const void* w, const float* w_scale, const void* bias, void* c,
+                                        void* stream) {
+    sdxl_hip::LnLinearParams p;
+    const sdxl_status st = ln_linear_params(d, x, gamma, beta, eps, w, w_scale, bias, c, true, p);
+    if (st != SDXL_STATUS_OK) return st;
+    if (p.m == 0 || p.n == 0) return SDXL_STATUS_OK;
+    return launch_status(sdxl_hip::launch_ln_linear(p, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                         "sdxl_layer_norm_linear_e4m3");
 }
 
 }  // extern "C"
@@ -309,17 +321,35 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     qd.k = W;
     qd.w_dtype = d->w_qkv_dtype;
     sdxl_status st;
-    if (act_fp8) {
+    // LayerNorm fused into the projection where the kernel takes the shape
+    // (E4M3 weights, width 640: the level-1 blocks); else two launches.
+    // (checked quietly: an unsupported shape is no error here)
+    sdxl_hip::LnLinearParams lp{};
+    lp.x = x;
+    lp.gamma = ln_gamma;
+    lp.beta = ln_beta;
+    lp.w = static_cast<const uint8_t*>(w_qkv);
+    lp.w_scale = w_qkv_scale;
+    lp.c = qkv;
+    lp.ldx = W;
+    lp.ldw = W;
+    lp.ldc = 3 * W;
+    lp.m = (int32_t)M;
+    lp.n = (int32_t)(3 * W);
+    lp.k = (int32_t)W;
+    lp.eps = d->ln_eps > 0.0f ? d->ln_eps : 1.0e-5f;
+    lp.a_fp8 = act_fp8 ? 1 : 0;
+    const bool fuse = d->ln_fusion == 0 && d->w_qkv_dtype == SDXL_DTYPE_E4M3 && M <= INT32_MAX &&
+                      3 * W <= INT32_MAX && x != nullptr && ln_gamma != nullptr && ln_beta != nullptr &&
+                      w_qkv != nullptr && sdxl_hip::ln_linear_supported(lp);
+    if (act_fp8 && fuse) {
+        st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
+                           "sdxl_attn_sublayer");
+    } else if (act_fp8) {
         st = sdxl_layer_norm_e4m3(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, codes, 0, code_scale, stream);
         if (st != SDXL_STATUS_OK) return st;
         st = sdxl_linear_e4m3(&qd, codes, code_scale, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
     } else {
-        // LayerNorm fused into the projection where the kernel takes the shape
-        // (E4M3 weights, width 640: the level-1 blocks); else two launches.
-        sdxl_hip::LnLinearParams lp;
-        const bool fuse = d->ln_fusion == 0 && d->w_qkv_dtype == SDXL_DTYPE_E4M3 &&
-                          ln_linear_params(&qd, x, ln_gamma, ln_beta, d->ln_eps, w_qkv, w_qkv_scale, nullptr, qkv,
-                                           lp) == SDXL_STATUS_OK;
         if (fuse) {
             st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
                                "sdxl_attn_sublayer");

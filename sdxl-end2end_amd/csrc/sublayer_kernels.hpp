@@ -70,6 +70,8 @@ struct LnLinearParams {
     int64_t ldx, ldw, ldc;
     int32_t m, n, k;
     float eps;
+    int32_t a_fp8;  // nonzero: the LayerNorm rounds its rows to E4M3 codes with per-row scales (as
+                    // launch_layer_norm's E4M3 output) and the projection runs on the fp8 matrix cores
     int32_t m_blocks, n_split, chunks;  // filled by the launcher
 };
 bool ln_linear_supported(const LnLinearParams& params);

@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "sdxl_linear",
     "sdxl_linear_e4m3",
     "sdxl_layer_norm_linear",
+    "sdxl_layer_norm_linear_e4m3",
     "sdxl_attn_sublayer_noalloc",
     "sdxl_attn_sublayer_noalloc_max_workspace_bytes",
     "sdxl_quantize_e4m3_rows",
@@ -137,6 +138,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sdxl_linear_e4m3.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, vp, vp, vp, vp, vp]
     lib.sdxl_layer_norm_linear.restype = ctypes.c_int
     lib.sdxl_layer_norm_linear.argtypes = [ctypes.POINTER(LinearDesc), vp, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp]
+    lib.sdxl_layer_norm_linear_e4m3.restype = ctypes.c_int
+    lib.sdxl_layer_norm_linear_e4m3.argtypes = lib.sdxl_layer_norm_linear.argtypes
     lib.sdxl_quantize_e4m3_rows.restype = ctypes.c_int
     lib.sdxl_quantize_e4m3_rows.argtypes = [i64, i64, vp, vp, vp, vp]
     lib.sdxl_attn_sublayer_workspace_bytes.restype = ctypes.c_size_t
@@ -320,10 +323,12 @@ def linear(a, w, w_scale=None, bias=None, residual=None, out=None):
     return out
 
 
-def layer_norm_linear(x, gamma, beta, w, w_scale, bias=None, eps: float = 1e-5, out=None):
+def layer_norm_linear(x, gamma, beta, w, w_scale, bias=None, eps: float = 1e-5, out=None,
+                      fp8_activations: bool = False):
     """LayerNorm fused into an E4M3-weight projection (sdxl_layer_norm_linear): x [M, K] fp16 (K = 640),
     w uint8 E4M3 [N, K] with w_scale [N]; returns LN(x) . w^T * w_scale + bias as fp16 [M, N], equal to
-    linear(layer_norm(x), w, w_scale, bias)."""
+    linear(layer_norm(x), w, w_scale, bias). fp8_activations: sdxl_layer_norm_linear_e4m3, equal to
+    linear_e4m3(*layer_norm_e4m3(x), w, w_scale, bias)."""
     import torch
     M, K = x.shape
     N = w.shape[0]
@@ -331,8 +336,9 @@ def layer_norm_linear(x, gamma, beta, w, w_scale, bias=None, eps: float = 1e-5, 
         out = torch.empty((M, N), dtype=torch.float16, device=x.device)
     d = LinearDesc(m=M, n=N, k=K, a_row_stride=x.stride(0), w_row_stride=w.stride(0), c_row_stride=out.stride(0),
                    residual_row_stride=0, w_dtype=E4M3, reserved=0)
-    _check(load().sdxl_layer_norm_linear(ctypes.byref(d), _ptr(x), _ptr(gamma), _ptr(beta), eps, _ptr(w),
-                                         _ptr(w_scale), _ptr(bias), _ptr(out), _stream(x)))
+    fn = load().sdxl_layer_norm_linear_e4m3 if fp8_activations else load().sdxl_layer_norm_linear
+    _check(fn(ctypes.byref(d), _ptr(x), _ptr(gamma), _ptr(beta), eps, _ptr(w), _ptr(w_scale), _ptr(bias), _ptr(out),
+              _stream(x)))
     return out
 
 

@@ -207,16 +207,47 @@ def test_layer_norm_linear(M, N, bias, strided):
     assert (err <= bound).all(), float(err.max())
 
 
+@pytest.mark.parametrize("M,N,bias", [(8192, 1920, False), (8100, 1920, True), (130, 3840, True), (1, 128, False),
+                                      (1000, 1920, False)])
+def test_layer_norm_linear_e4m3_activations(M, N, bias):
+    """sdxl_layer_norm_linear_e4m3 (E4M3 LayerNorm rows with per-row scales, fp8 MFMA, inside one
+    kernel) equals sdxl_layer_norm_e4m3 followed by sdxl_linear_e4m3 bit for bit; the product
+    part against the fp64 product of the decoded codes (the E4M3 LayerNorm itself is pinned to
+    the oracle by test_layer_norm_e4m3)."""
+    K = 640
+    print(f"ln_linear e4m3 M{M} N{N} bias{bias}", flush=True)
+    xb = oracle.normal_f16(1120 + M, (M, K))
+    gb = oracle.normal_f16(1121, (K,), 0.5)
+    bb = oracle.normal_f16(1122, (K,), 0.5)
+    q, s = oracle.quantize_e4m3_rows(oracle.normal_f32(1123 + N, (N, K), 0.02))
+    biasb = oracle.normal_f16(1124, (N,), 0.02) if bias else None
+    x, g, b = dev16(xb), dev16(gb), dev16(bb)
+    wq, ws = torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV)
+    bias_t = dev16(biasb) if bias else None
+    got = sh.layer_norm_linear(x, g, b, wq, ws, bias=bias_t, fp8_activations=True)
+    codes, cs = sh.layer_norm_e4m3(x, g, b)
+    comp = sh.linear_e4m3(codes, cs, wq, ws, bias=bias_t)
+    torch.cuda.synchronize()
+    assert torch.equal(got, comp)
+    rows = np.r_[0:64, M // 2:M // 2 + 32, M - 70:M] if M > 256 else np.arange(M)
+    ref = oracle.dequantize_e4m3_rows(codes.cpu().numpy()[rows], cs.cpu().numpy()[rows]).astype(np.float64) @ \
+        oracle.dequantize_e4m3_rows(q, s).astype(np.float64).T
+    if bias:
+        ref = ref + oracle.f16_bits_to_f32(biasb)[None, :]
+    within_half_ulp(host(got)[rows], ref, 1e-4, f"LN E4M3 + linear {M}x{N}")
+
+
 def test_sublayer_layer_norm_fusion_switch():
     """configs[3] sublayer with the LayerNorm inside the q|k|v projection (default) and as its own
-    launch (ln_fusion off): the same bits."""
+    launch (ln_fusion off), fp16 and E4M3 activations: the same bits."""
     x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(2, 4096, 10, 1110)
     gamma = dev16(oracle.normal_f16(1111, (640,), 0.5))
     beta = dev16(oracle.normal_f16(1112, (640,), 0.5))
-    y1 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10)
-    y2 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, ln_fusion=False)
-    torch.cuda.synchronize()
-    assert torch.equal(y1, y2)
+    for fp8 in (False, True):
+        y1 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, fp8_activations=fp8)
+        y2 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, fp8_activations=fp8, ln_fusion=False)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), fp8
 
 
 # ---------------------------------------------------------------- sublayer (configs[3])
