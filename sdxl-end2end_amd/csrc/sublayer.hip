@@ -785,43 +785,63 @@ __device__ __forceinline__ float row16_max(float x) {
 // LayerNorm statistics of four rows per wave for widths that are a multiple of
 // 128: lane l works on row l / 16 and holds its 16-byte chunks l % 16 + 16 i
 // (i < kCpl = width / 128), so every lane is busy and a row's sums need no
-// cross-row exchange. Two-pass centred variance, every operation rounded on its
-// own (as ln_row_stats_v8). v receives the row's values in fp32.
+// cross-row exchange. Two-pass centred variance in fp32 (the reference's
+// form, ops_kernels.cu:225-257): the sum by v_dot2 of fp16 pairs against ones
+// (exact products, fp32 accumulation), the centred values x - mean straight
+// from fp16 (one fused multiply-add with 1, the exact difference rounded
+// once), their squares by fused multiply-adds. d receives the centred values.
 template <int kCpl>
-__device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float eps, float (&v)[8 * kCpl], float& mean,
-                                               float& inv) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float eps, float (&d)[8 * kCpl], float& inv) {
     constexpr int kWidth = 128 * kCpl;
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     float sum = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            v[8 * i + e] = (float)h[i][e];
-            sum += v[8 * i + e];
-        }
-    mean = row16_sum(sum) / (float)kWidth;
+        for (int e = 0; e < 8; e += 2)
+            sum = __builtin_amdgcn_fdot2(f16x2{h[i][e], h[i][e + 1]}, ones, sum, false);
+    const float mean = row16_sum(sum) / (float)kWidth;
     float sq = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8 * kCpl; ++k) {
-        const float d = v[k] - mean;
-        sq += d * d;
-    }
+    for (int i = 0; i < kCpl; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            d[8 * i + e] = __builtin_fmaf((float)h[i][e], 1.0f, -mean);
+            sq = __builtin_fmaf(d[8 * i + e], d[8 * i + e], sq);
+        }
     const float var = fmaxf(row16_sum(sq) / (float)kWidth, 0.0f);
     inv = 1.0f / sqrtf(var + eps);
 }
 
+// One normalised value of the four-rows form in fp32: (d * inv) * gamma + beta
+// with the last two as one fused multiply-add.
+__device__ __forceinline__ float ln4_affine(float d, float inv, _Float16 g, _Float16 b) {
+    return __builtin_fmaf(d * inv, (float)g, (float)b);
+}
+
 // fp16 LayerNorm of four rows per wave (ln_rows4_stats); writes the normalised
-// chunks through put(i, chunk index, value).
+// chunks through put(i, chunk index, value). Each value is rounded to fp32 and
+// then to fp16 (the empty asm keeps the compiler from folding the fma and the
+// conversion into one v_fma_mix rounding, which it may do in one caller and not
+// in another).
 template <int kCpl, typename Put>
 __device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl], const f16x8v (&bb)[kCpl],
                                          float eps, Put&& put) {
-    float v[8 * kCpl];
-    float mean, inv;
-    ln_rows4_stats<kCpl>(h, eps, v, mean, inv);
+    float d[8 * kCpl];
+    float inv;
+    ln_rows4_stats<kCpl>(h, eps, d, inv);
     const int j = threadIdx.x & 15;
 #pragma unroll
-    for (int i = 0; i < kCpl; ++i) put(i, j + 16 * i, ln_out_v8(v + 8 * i, mean, inv, gg[i], bb[i]));
+    for (int i = 0; i < kCpl; ++i) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = ln4_affine(d[8 * i + e], inv, gg[i][e], bb[i][e]);
+        asm volatile("" : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]), "+v"(y[6]), "+v"(y[7]));
+        f16x8v o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (_Float16)y[e];
+        put(i, j + 16 * i, o);
+    }
 }
 
 // E4M3 codes of four values y / scale (r = 1 / scale, correctly rounded): the
@@ -838,23 +858,22 @@ __device__ __forceinline__ uint32_t e4m3_code4(const float* y4, float scale, flo
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
 }
 
-// E4M3 LayerNorm of four rows per wave: the normalised fp32 row (ln_affine),
+// E4M3 LayerNorm of four rows per wave: the normalised fp32 row (ln4_affine),
 // its scale max(amax / 448, 1e-12) (1 for an all-zero row) and the codes
 // E4M3(y / scale) (the weight quantiser's rule). put(i, chunk index, 8 codes as
 // two dwords); returns the row's scale (the same in all 16 lanes of the row).
 template <int kCpl, typename Put>
 __device__ __forceinline__ float ln_rows4_e4m3(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl],
                                                const f16x8v (&bb)[kCpl], float eps, Put&& put) {
-#pragma clang fp contract(off)
     float v[8 * kCpl];
-    float mean, inv;
-    ln_rows4_stats<kCpl>(h, eps, v, mean, inv);
+    float inv;
+    ln_rows4_stats<kCpl>(h, eps, v, inv);
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            v[8 * i + e] = ln_affine(v[8 * i + e], mean, inv, gg[i][e], bb[i][e]);
+            v[8 * i + e] = ln4_affine(v[8 * i + e], inv, gg[i][e], bb[i][e]);
             amax = fmaxf(amax, fabsf(v[8 * i + e]));
         }
     amax = row16_max(amax);
@@ -1057,14 +1076,21 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     issue_stage(0);
     if (G > 1) issue_stage(1);
 
-    // Per-column scales and bias of the workgroup's columns, once.
+    // Per-column scales and bias of the workgroup's columns: loaded now, with
+    // the rows below, and written to LDS after the LayerNorm (one memory round
+    // trip for both).
+    constexpr int kColsPerThread = kLnLinMaxCols / 512;
+    float sc_reg[kColsPerThread], bias_reg[kColsPerThread];
     {
         const int n0 = c_begin * 128, ncols = nch * 128;
-        for (int i = threadIdx.x; i < ncols; i += 512) {
-            sc_lds[i] = p.w_scale[n0 + i];
-            bias_lds[i] = p.bias != nullptr ? (float)((const _Float16*)p.bias)[n0 + i] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < kColsPerThread; ++k) {
+            const int i = threadIdx.x + 512 * k;
+            sc_reg[k] = i < ncols ? p.w_scale[n0 + i] : 0.0f;
+            bias_reg[k] = i < ncols && p.bias != nullptr ? (float)((const _Float16*)p.bias)[n0 + i] : 0.0f;
         }
     }
+
 
     // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7 as two groups
     // of four, ln_rows4: the standalone LayerNorm's arithmetic; rows past m
@@ -1105,6 +1131,11 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
                 });
             }
         }
+    }
+#pragma unroll
+    for (int k = 0; k < kColsPerThread; ++k) {
+        sc_lds[threadIdx.x + 512 * k] = sc_reg[k];
+        bias_lds[threadIdx.x + 512 * k] = bias_reg[k];
     }
     __syncthreads();
     // Activation operands of the wave's rows: step ks = 4 s + 2 pp + q (s: 64-column
