@@ -163,7 +163,7 @@ def test_linear_strided_in_place_residual():
 @pytest.mark.parametrize("M,N,bias,strided", [(8192, 1920, False, False), (8100, 1920, True, False),
                                               (200, 640, True, True), (1, 128, False, False),
                                               (4096, 128, False, True), (130, 3840, True, False),
-                                              (1000, 1920, False, False)])
+                                              (1000, 1920, False, False), (15360, 1920, True, False)])
 def test_layer_norm_linear(M, N, bias, strided):
     """sdxl_layer_norm_linear (norm1 -> q|k|v at width 640) equals sdxl_layer_norm followed by
     sdxl_linear bit for bit (same LayerNorm rounding, same fp32 sums), and the oracle's fp32
@@ -171,7 +171,8 @@ def test_layer_norm_linear(M, N, bias, strided):
     weights, within the linear bar. Non-trivial gamma/beta; ragged row blocks (8100, 200, 130,
     1); one- and several-chunk column ranges, uneven splits (1000 rows: 15 chunks over 16
     workgroups of a row block is capped at one chunk each; 130 x 3840: 30 chunks, two
-    workgroups of at most 2048 columns); strided x and c."""
+    workgroups of at most 2048 columns; 15360 rows, configs[4]'s level 1: 240 row blocks, every
+    workgroup on all 15 chunks); strided x and c."""
     K = 640
     print(f"ln_linear M{M} N{N} bias{bias} strided{strided}", flush=True)
     xb = oracle.normal_f16(1100 + M, (M, K))
@@ -208,7 +209,7 @@ def test_layer_norm_linear(M, N, bias, strided):
 
 
 @pytest.mark.parametrize("M,N,bias", [(8192, 1920, False), (8100, 1920, True), (130, 3840, True), (1, 128, False),
-                                      (1000, 1920, False)])
+                                      (1000, 1920, False), (15360, 1920, False)])
 def test_layer_norm_linear_e4m3_activations(M, N, bias):
     """sdxl_layer_norm_linear_e4m3 (E4M3 LayerNorm rows with per-row scales, fp8 MFMA, inside one
     kernel) equals sdxl_layer_norm_e4m3 followed by sdxl_linear_e4m3 bit for bit; the product
