@@ -80,7 +80,8 @@ def test_quantizer_matches_oracle_bit_exact():
 
 # ---------------------------------------------------------------- LayerNorm
 
-@pytest.mark.parametrize("rows,width", [(8192, 640), (77, 320), (5, 1280), (3, 2048), (1, 128), (4, 66)])
+@pytest.mark.parametrize("rows,width", [(8192, 640), (77, 320), (5, 1280), (3, 2048), (1, 128), (4, 66), (77, 640),
+                                        (19, 256)])
 def test_layer_norm(rows, width):
     xb = oracle.normal_f16(920 + width, (rows, width))
     gb = oracle.normal_f16(921, (width,), 0.5)
@@ -339,7 +340,8 @@ def e4m3_half_step(v):
     return 2.0 ** (e - 3) / 2
 
 
-@pytest.mark.parametrize("rows,width", [(8192, 640), (77, 320), (5, 1280), (3, 2048), (4, 66)])
+@pytest.mark.parametrize("rows,width", [(8192, 640), (77, 320), (5, 1280), (3, 2048), (4, 66), (77, 640),
+                                        (19, 256)])
 def test_layer_norm_e4m3(rows, width):
     xb = oracle.normal_f16(990 + width, (rows, width))
     gb = oracle.normal_f16(991, (width,), 0.5)
