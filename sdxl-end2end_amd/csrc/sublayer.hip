@@ -1004,17 +1004,21 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
 //
 // One workgroup of 8 waves per CU (two per SIMD) owns 64 rows and a range of
 // 128-column chunks of the output. Prologue: the rows are normalised once
-// (one wave per row, the LayerNorm kernel's arithmetic) into LDS, then each
-// wave takes its 32 rows' normalised values into registers as MFMA operands
-// (kK / 16 steps of 8 values: 160 VGPRs at kK = 640), so the activations
-// never go back to HBM and are read from LDS once. Main loop: the E4M3 weight
+// (four rows per wave, ln_rows4: the standalone LayerNorm kernel's code) into
+// LDS, then each wave takes its 32 rows' normalised values into registers as
+// MFMA operands (kK / 16 steps of 8 values: 160 VGPRs at kK = 640), so the
+// activations never go back to HBM and are read from LDS once. kAFp8: the
+// LayerNorm rounds each row to E4M3 codes with a per-row scale (ln_rows4_e4m3,
+// the standalone E4M3 LayerNorm's code; 80 VGPRs of codes) and the projection
+// runs on v_mfma_f32_32x32x64_f8f6f4 with the weight codes as read (no
+// decode), as linear_kernel's fp8 form. Main loop: the E4M3 weight
 // rows of each chunk stream HBM/L2 -> LDS by global_load_lds_dwordx4 in
 // 128-column K stages (two 64-byte-row sub-stages, linear_kernel's layout)
 // through a ring of three (prefetch distance two, one barrier per stage);
 // wave (wm, wn) computes rows 32 wm .. +31 x columns 32 wn .. +31 of a chunk
 // as one chain of kK / 16 v_mfma_f32_32x32x16_f16 over linear_kernel's K
-// order, operand layouts and code decode, so the fp32 sums equal that
-// kernel's. A chunk's output is written (LDS-staged, 64-byte row segments)
+// order, operand layouts and code decode (fp8: one MFMA per 64-column
+// sub-stage), so the fp32 sums equal that kernel's. A chunk's output is written (LDS-staged, 64-byte row segments)
 // during the next chunk's second stage, so the stores drain under MFMA work
 // instead of in one burst at the end. Per-column scales and bias sit in LDS,
 // and every lane stores (rows past m repeat row m - 1 with its own value), so
@@ -1090,7 +1094,6 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
             bias_reg[k] = i < ncols && p.bias != nullptr ? (float)((const _Float16*)p.bias)[n0 + i] : 0.0f;
         }
     }
-
 
     // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7 as two groups
     // of four, ln_rows4: the standalone LayerNorm's arithmetic; rows past m
