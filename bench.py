@@ -44,7 +44,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,qkv,qkv_fp8,ln_qkv) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -426,7 +426,7 @@ def main():
     if args.only == "vae":
         print(json.dumps(bench_vae_attention(torch, sh, args.steps, args.warmup)), flush=True)
         return
-    if args.only in ("qkv", "qkv_fp8", "ln_qkv"):
+    if args.only in ("qkv", "qkv_fp8", "ln_qkv", "ln_qkv_fp8"):
         # profiling aid: the configs[3] QKV projection alone, eager launches (E4M3 weights [1920, 640];
         # fp16 activations on fp16 MFMA, or E4M3 activations on fp8 MFMA)
         M, W = 8192, 640
@@ -437,10 +437,11 @@ def main():
         out = torch.empty(M, 3 * W, dtype=torch.float16, device="cuda:0")
         if args.only == "qkv":
             fn = lambda: sh.linear(a, q8, w_scale=s8, out=out)
-        elif args.only == "ln_qkv":  # LayerNorm inside the projection (sdxl_layer_norm_linear)
+        elif args.only in ("ln_qkv", "ln_qkv_fp8"):  # LayerNorm inside the projection (sdxl_layer_norm_linear[_e4m3])
             ones = torch.ones(W, dtype=torch.float16, device="cuda:0")
             zeros = torch.zeros(W, dtype=torch.float16, device="cuda:0")
-            fn = lambda: sh.layer_norm_linear(a, ones, zeros, q8, s8, out=out)
+            fp8 = args.only == "ln_qkv_fp8"
+            fn = lambda: sh.layer_norm_linear(a, ones, zeros, q8, s8, out=out, fp8_activations=fp8)
         else:
             codes, cs = sh.layer_norm_e4m3(a.view(1, M, W), torch.ones(W, dtype=torch.float16, device="cuda:0"),
                                            torch.zeros(W, dtype=torch.float16, device="cuda:0"))
