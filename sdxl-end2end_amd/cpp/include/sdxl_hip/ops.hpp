@@ -38,6 +38,14 @@ public:
     // fp16 bias [N]. K % 64 == 0, N % 4 == 0.
     [[nodiscard]] Tensor linear(const Tensor& input, const Tensor& weight, const Tensor* bias = nullptr) const;
 
+    // linear(layer_norm(input, norm_weight, norm_bias, epsilon), weight, bias) — the
+    // transformer block's norm -> projection (unet.cpp:106-112) — in one launch where the
+    // fused kernel takes the shape (Float8E4M3 weight, width 640, N % 128 == 0: the
+    // level-1 q|k|v), else as the two calls; the same result either way.
+    [[nodiscard]] Tensor layer_norm_linear(const Tensor& input, const Tensor& norm_weight, const Tensor& norm_bias,
+                                           const Tensor& weight, const Tensor* bias = nullptr,
+                                           float epsilon = 1.0e-5F) const;
+
     // hidden += input . weight^T + bias in one pass (the reference's linear followed by
     // add_in_place, unet.cpp:114-118, with the residual added in the linear's epilogue).
     void linear_residual_into(const Tensor& input, const Tensor& weight, const Tensor* bias, Tensor& hidden) const;

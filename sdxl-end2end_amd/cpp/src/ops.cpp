@@ -150,6 +150,29 @@ Tensor Ops::linear(const Tensor& input, const Tensor& weight, const Tensor* bias
     return output;
 }
 
+Tensor Ops::layer_norm_linear(const Tensor& input, const Tensor& norm_weight, const Tensor& norm_bias,
+                              const Tensor& weight, const Tensor* bias, float epsilon) const {
+    const sdxl_linear_desc d = linear_desc(input, weight);
+    check_bias(bias, weight.size(0));
+    if (norm_weight.type() != ScalarType::Float16 || norm_bias.type() != ScalarType::Float16 ||
+        norm_weight.rank() != 1 || norm_bias.rank() != 1 || norm_weight.size(0) != input.shape().back() ||
+        norm_bias.size(0) != input.shape().back())
+        throw HipError("CUDA layer norm shape/type mismatch");
+    const bool fused = d.w_dtype == SDXL_DTYPE_E4M3 && d.k == 640 && d.n % 128 == 0;
+    if (!fused) return linear(layer_norm(input, norm_weight, norm_bias, epsilon), weight, bias);
+    std::vector<std::size_t> shape = input.shape();
+    shape.back() = weight.size(0);
+    Tensor output = Tensor::allocate(*runtime_, shape, ScalarType::Float16);
+    const int scope = runtime_->begin_profile("ops/layer_norm_linear/e4m3/m" + std::to_string(d.m) + "_n" +
+                                              std::to_string(d.n) + "_k" + std::to_string(d.k));
+    const sdxl_status st = sdxl_layer_norm_linear(&d, input.data(), norm_weight.data(), norm_bias.data(), epsilon,
+                                                  weight.data(), weight.dequant_scale_data(),
+                                                  bias ? bias->data() : nullptr, output.data(), runtime_->stream());
+    runtime_->end_profile(scope);
+    check(st);
+    return output;
+}
+
 void Ops::linear_residual_into(const Tensor& input, const Tensor& weight, const Tensor* bias, Tensor& hidden) const {
     const sdxl_linear_desc d = linear_desc(input, weight);
     check_bias(bias, weight.size(0));

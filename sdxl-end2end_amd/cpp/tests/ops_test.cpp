@@ -137,6 +137,31 @@ void sublayer_cases() {
                    "linear feature mismatch", "linear shape");
     require_throws([&] { (void)ops.layer_norm(xd, wd, wd); }, "CUDA layer norm shape/type mismatch", "layer_norm shape");
 
+    // layer_norm_linear at width 640 (the fused kernel) equals layer_norm -> linear bit for bit
+    {
+        const std::size_t W6 = 640, N6 = 1920;
+        const auto x6 = filled({2, rows / 2, W6}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.29F) * 1.5F; });
+        const auto g6 = filled({W6}, [](std::size_t i) { return 1.0F + 0.25F * std::cos(static_cast<float>(i)); });
+        const auto b6 = filled({W6}, [](std::size_t i) { return 0.1F * std::sin(static_cast<float>(i)); });
+        const auto w6 = filled({N6, W6}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.013F) * 0.04F; });
+        auto x6d = Tensor::from_host_f32(runtime, x6);
+        auto g6d = Tensor::from_host_f32(runtime, g6), b6d = Tensor::from_host_f32(runtime, b6);
+        const auto w6p = ops.pack_e4m3(Tensor::from_host_f32(runtime, w6));
+        const auto fused = ops.layer_norm_linear(x6d, g6d, b6d, w6p).to_host_f32(runtime);
+        const auto comp = ops.linear(ops.layer_norm(x6d, g6d, b6d), w6p).to_host_f32(runtime);
+        require(fused.values.size() == comp.values.size(), "layer_norm_linear shape");
+        for (std::size_t i = 0; i < comp.values.size(); ++i)
+            require(std::memcmp(&fused.values[i], &comp.values[i], sizeof(float)) == 0,
+                    "layer_norm_linear equals layer_norm -> linear");
+        // fp16 weight (no fused kernel): the two calls
+        auto onesd = Tensor::from_host_f32(runtime, ones), zerosd = Tensor::from_host_f32(runtime, zeros);
+        const auto unfused = ops.layer_norm_linear(xd, onesd, zerosd, wd).to_host_f32(runtime);
+        const auto unfused_ref = ops.linear(ops.layer_norm(xd, onesd, zerosd), wd).to_host_f32(runtime);
+        for (std::size_t i = 0; i < unfused_ref.values.size(); ++i)
+            require(std::memcmp(&unfused.values[i], &unfused_ref.values[i], sizeof(float)) == 0,
+                    "layer_norm_linear with an fp16 weight equals the two calls");
+    }
+
     // attention_sublayer == layer_norm -> linear(qkv) -> attention -> linear_residual_into
     const std::size_t heads = 2;
     const auto wq = filled({3 * W, W}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.013F) * 0.06F; });
