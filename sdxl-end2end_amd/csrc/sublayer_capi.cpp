@@ -251,10 +251,6 @@ sdxl_status sdxl_layer_norm_linear_e4m3(const sdxl_linear_desc* d, const void* x
                          "sdxl_layer_norm_linear_e4m3");
 }
 
-}  // extern "C"
-
-extern "C" {
-
 sdxl_status sdxl_linear(const sdxl_linear_desc* d, const void* a, const void* w, const float* w_scale,
                         const void* bias, const void* residual, void* c, void* stream) {
     return linear_impl(d, a, nullptr, w, w_scale, bias, residual, c, stream);
@@ -342,7 +338,7 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     const bool fuse = d->ln_fusion == 0 && d->w_qkv_dtype == SDXL_DTYPE_E4M3 && M <= INT32_MAX &&
                       3 * W <= INT32_MAX && x != nullptr && ln_gamma != nullptr && ln_beta != nullptr &&
                       w_qkv != nullptr && sdxl_hip::ln_linear_supported(lp);
-    if (act_fp8 && fuse) {
+    if (fuse) {
         st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
                            "sdxl_attn_sublayer");
     } else if (act_fp8) {
@@ -350,14 +346,9 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
         if (st != SDXL_STATUS_OK) return st;
         st = sdxl_linear_e4m3(&qd, codes, code_scale, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
     } else {
-        if (fuse) {
-            st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
-                               "sdxl_attn_sublayer");
-        } else {
-            st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
-            if (st != SDXL_STATUS_OK) return st;
-            st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
-        }
+        st = sdxl_layer_norm(M, W, x, 0, ln_gamma, ln_beta, d->ln_eps, hidden_ws, 0, stream);
+        if (st != SDXL_STATUS_OK) return st;
+        st = sdxl_linear(&qd, hidden_ws, w_qkv, w_qkv_scale, nullptr, nullptr, qkv, stream);
     }
     if (st != SDXL_STATUS_OK) return st;
 
