@@ -782,17 +782,27 @@ __device__ __forceinline__ float row16_max(float x) {
     return x;
 }
 
-// LayerNorm statistics of four rows per wave for widths that are a multiple of
-// 128: lane l works on row l / 16 and holds its 16-byte chunks l % 16 + 16 i
-// (i < kCpl = width / 128), so every lane is busy and a row's sums need no
-// cross-row exchange. Two-pass centred variance in fp32 (the reference's
-// form, ops_kernels.cu:225-257): the sum by v_dot2 of fp16 pairs against ones
-// (exact products, fp32 accumulation), the centred values x - mean straight
-// from fp16 (one fused multiply-add with 1, the exact difference rounded
-// once), their squares by fused multiply-adds. d receives the centred values.
-template <int kCpl>
+// Sum over each 32-lane half of the wave: the 16-lane butterfly, then the two
+// 16-lane rows of a half exchanged (commutative, so both hold the same value).
+__device__ __forceinline__ float row32_sum(float x) {
+    x = row16_sum(x);
+    return x + __shfl_xor(x, 16, 64);
+}
+
+// LayerNorm statistics of 64 / kLanes rows per wave (kLanes = 16 or 32 lanes
+// per row) for widths 8 kLanes kCpl: lane l works on row l / kLanes and holds
+// its 16-byte chunks l % kLanes + kLanes i (i < kCpl), so every lane is busy and
+// a row's sums stay inside its lane group. Two-pass centred variance in fp32
+// (the reference's form, ops_kernels.cu:225-257): the sum by v_dot2 of fp16
+// pairs against ones (exact products, fp32 accumulation), the centred values
+// x - mean straight from fp16 (one fused multiply-add with 1, the exact
+// difference rounded once), their squares by fused multiply-adds. d receives
+// the centred values.
+template <int kCpl, int kLanes = 16>
 __device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float eps, float (&d)[8 * kCpl], float& inv) {
-    constexpr int kWidth = 128 * kCpl;
+    static_assert(kLanes == 16 || kLanes == 32, "16 or 32 lanes per row");
+    constexpr int kWidth = 8 * kLanes * kCpl;
+    auto rsum = [](float x) __attribute__((always_inline)) { return kLanes == 16 ? row16_sum(x) : row32_sum(x); };
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     float sum = 0.0f;
 #pragma unroll
@@ -800,7 +810,7 @@ __device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float ep
 #pragma unroll
         for (int e = 0; e < 8; e += 2)
             sum = __builtin_amdgcn_fdot2(f16x2{h[i][e], h[i][e + 1]}, ones, sum, false);
-    const float mean = row16_sum(sum) / (float)kWidth;
+    const float mean = rsum(sum) / (float)kWidth;
     float sq = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
@@ -809,7 +819,7 @@ __device__ __forceinline__ void ln_rows4_stats(const f16x8v (&h)[kCpl], float ep
             d[8 * i + e] = __builtin_fmaf((float)h[i][e], 1.0f, -mean);
             sq = __builtin_fmaf(d[8 * i + e], d[8 * i + e], sq);
         }
-    const float var = fmaxf(row16_sum(sq) / (float)kWidth, 0.0f);
+    const float var = fmaxf(rsum(sq) / (float)kWidth, 0.0f);
     inv = 1.0f / sqrtf(var + eps);
 }
 
@@ -819,18 +829,18 @@ __device__ __forceinline__ float ln4_affine(float d, float inv, _Float16 g, _Flo
     return __builtin_fmaf(d * inv, (float)g, (float)b);
 }
 
-// fp16 LayerNorm of four rows per wave (ln_rows4_stats); writes the normalised
-// chunks through put(i, chunk index, value). Each value is rounded to fp32 and
-// then to fp16 (the empty asm keeps the compiler from folding the fma and the
-// conversion into one v_fma_mix rounding, which it may do in one caller and not
-// in another).
-template <int kCpl, typename Put>
+// fp16 LayerNorm of 64 / kLanes rows per wave (ln_rows4_stats); writes the
+// normalised chunks through put(i, chunk index, value). Each value is rounded to
+// fp32 and then to fp16 (the empty asm keeps the compiler from folding the fma
+// and the conversion into one v_fma_mix rounding, which it may do in one
+// caller and not in another).
+template <int kCpl, int kLanes = 16, typename Put>
 __device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl], const f16x8v (&bb)[kCpl],
                                          float eps, Put&& put) {
     float d[8 * kCpl];
     float inv;
-    ln_rows4_stats<kCpl>(h, eps, d, inv);
-    const int j = threadIdx.x & 15;
+    ln_rows4_stats<kCpl, kLanes>(h, eps, d, inv);
+    const int j = threadIdx.x & (kLanes - 1);
 #pragma unroll
     for (int i = 0; i < kCpl; ++i) {
         float y[8];
@@ -840,7 +850,7 @@ __device__ __forceinline__ void ln_rows4(const f16x8v (&h)[kCpl], const f16x8v (
         f16x8v o;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = (_Float16)y[e];
-        put(i, j + 16 * i, o);
+        put(i, j + kLanes * i, o);
     }
 }
 
@@ -906,6 +916,31 @@ __global__ __launch_bounds__(256) void layer_norm_r4_kernel(LayerNormParams p) {
     }
     f16x8v* y = (f16x8v*)((_Float16*)p.y + r * p.ldy);
     ln_rows4<kCpl>(h, gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
+        if (row < p.rows) store_out<kNt>(o, y + c);
+    });
+}
+
+// fp16 LayerNorm for widths 256 kCpl: 8 rows per 256-thread block, two per
+// wave with 32 lanes per row (the level-2 rows, 1280 = 256 x 5, hold as many
+// values per lane as the width-640 rows in the four-rows form).
+template <int kCpl, bool kNt>
+__global__ __launch_bounds__(256) void layer_norm_r2_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t r = row < p.rows ? row : p.rows - 1;  // rows past the end repeat the last (not stored)
+    const int j = lane & 31;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + r * p.ldx);
+    const f16x8v* g = (const f16x8v*)p.gamma;
+    const f16x8v* bt = (const f16x8v*)p.beta;
+    f16x8v h[kCpl], gg[kCpl], bb[kCpl];
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i) {
+        h[i] = x[j + 32 * i];
+        gg[i] = g[j + 32 * i];
+        bb[i] = bt[j + 32 * i];
+    }
+    f16x8v* y = (f16x8v*)((_Float16*)p.y + r * p.ldy);
+    ln_rows4<kCpl, 32>(h, gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
         if (row < p.rows) store_out<kNt>(o, y + c);
     });
 }
@@ -1510,6 +1545,23 @@ hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t strea
         break;
             SDXL_LNR4(1) SDXL_LNR4(2) SDXL_LNR4(3) SDXL_LNR4(4) SDXL_LNR4(5)
 #undef SDXL_LNR4
+        }
+        return hipGetLastError();
+    }
+    // Two rows per wave (32 lanes per row) for fp16 widths 768 .. 1280 in steps of
+    // 256 (the level-2 rows).
+    if (!e4m3 && p.width % 256 == 0 && p.width > 640 && p.width <= 1280 && p.ldx % 8 == 0 &&
+        ((uintptr_t)p.x & 15) == 0 && ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 &&
+        p.ldy % 8 == 0 && ((uintptr_t)p.y & 15) == 0) {
+        const dim3 g8((unsigned)((p.rows + 7) / 8));
+        switch (p.width / 256) {
+#define SDXL_LNR2(n)                                                                            \
+    case n:                                                                                     \
+        if (nt) hipLaunchKernelGGL((layer_norm_r2_kernel<n, true>), g8, block, 0, stream, p);   \
+        else hipLaunchKernelGGL((layer_norm_r2_kernel<n, false>), g8, block, 0, stream, p);     \
+        break;
+            SDXL_LNR2(3) SDXL_LNR2(4) SDXL_LNR2(5)
+#undef SDXL_LNR2
         }
         return hipGetLastError();
     }
