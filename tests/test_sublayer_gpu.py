@@ -91,6 +91,32 @@ def test_layer_norm(rows, width):
     within_half_ulp(got, ref, 1e-5, f"LN {rows}x{width}")
 
 
+@pytest.mark.parametrize("width", [640, 1280])
+def test_layer_norm_large_mean(width):
+    """Rows of mean ~100 with unit spread (the centred variance must not cancel), and a constant
+    row (variance 0: y = beta): the four-rows / two-rows kernels against the oracle, fp16 and E4M3."""
+    rows = 48
+    xf = oracle.f16_bits_to_f32(oracle.normal_f16(1130 + width, (rows, width))) + np.float32(100.0)
+    xf[5, :] = 3.25
+    xb = f16(xf)
+    gb = oracle.normal_f16(1131, (width,), 0.5)
+    bb = oracle.normal_f16(1132, (width,), 0.5)
+    ref = oracle.layer_norm(oracle.f16_bits_to_f32(xb), oracle.f16_bits_to_f32(gb), oracle.f16_bits_to_f32(bb))
+    got = host(sh.layer_norm(dev16(xb), dev16(gb), dev16(bb)))
+    within_half_ulp(got, ref, 2e-5, f"LN large mean {width}")
+    q, s = sh.layer_norm_e4m3(dev16(xb), dev16(gb), dev16(bb))
+    torch.cuda.synchronize()
+    q_ref, s_ref = oracle.quantize_e4m3_rows(ref)
+    s_got = s.cpu().numpy()
+    np.testing.assert_allclose(s_got, s_ref, rtol=1e-5)
+    y = oracle.e4m3_table()[q.cpu().numpy()] * s_got[:, None]
+    err = np.abs(y.astype(np.float64) - ref)
+    # as test_layer_norm_e4m3: half an E4M3 step of y / scale, 5 % for rounding ties
+    bound = e4m3_half_step(ref / s_ref[:, None]) * s_ref[:, None] * 1.05 + 1e-6 * np.abs(ref) + 1e-7
+    assert (err <= bound).all(), float(err.max())
+    assert (q.cpu().numpy() == q_ref).mean() >= 0.9999
+
+
 def test_layer_norm_strided_in_place():
     base = dev16(oracle.normal_f16(925, (50, 768)))
     x = base[:, :640]
