@@ -868,16 +868,17 @@ __device__ __forceinline__ uint32_t e4m3_code4(const float* y4, float scale, flo
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(q[2], q[3], lo, true);
 }
 
-// E4M3 LayerNorm of four rows per wave: the normalised fp32 row (ln4_affine),
-// its scale max(amax / 448, 1e-12) (1 for an all-zero row) and the codes
-// E4M3(y / scale) (the weight quantiser's rule). put(i, chunk index, 8 codes as
-// two dwords); returns the row's scale (the same in all 16 lanes of the row).
-template <int kCpl, typename Put>
+// E4M3 LayerNorm of 64 / kLanes rows per wave: the normalised fp32 row
+// (ln4_affine), its scale max(amax / 448, 1e-12) (1 for an all-zero row) and
+// the codes E4M3(y / scale) (the weight quantiser's rule). put(i, chunk index,
+// 8 codes as two dwords); returns the row's scale (the same in all lanes of
+// the row).
+template <int kCpl, int kLanes = 16, typename Put>
 __device__ __forceinline__ float ln_rows4_e4m3(const f16x8v (&h)[kCpl], const f16x8v (&gg)[kCpl],
                                                const f16x8v (&bb)[kCpl], float eps, Put&& put) {
     float v[8 * kCpl];
     float inv;
-    ln_rows4_stats<kCpl>(h, eps, v, inv);
+    ln_rows4_stats<kCpl, kLanes>(h, eps, v, inv);
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
@@ -887,12 +888,13 @@ __device__ __forceinline__ float ln_rows4_e4m3(const f16x8v (&h)[kCpl], const f1
             amax = fmaxf(amax, fabsf(v[8 * i + e]));
         }
     amax = row16_max(amax);
+    if constexpr (kLanes == 32) amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     const float scale = amax > 0.0f ? fmaxf(amax / 448.0f, 1.0e-12f) : 1.0f;
     const float r = 1.0f / scale;
-    const int j = threadIdx.x & 15;
+    const int j = threadIdx.x & (kLanes - 1);
 #pragma unroll
     for (int i = 0; i < kCpl; ++i)
-        put(i, j + 16 * i, u32x2{e4m3_code4(v + 8 * i, scale, r), e4m3_code4(v + 8 * i + 4, scale, r)});
+        put(i, j + kLanes * i, u32x2{e4m3_code4(v + 8 * i, scale, r), e4m3_code4(v + 8 * i + 4, scale, r)});
     return scale;
 }
 
@@ -943,6 +945,30 @@ __global__ __launch_bounds__(256) void layer_norm_r2_kernel(LayerNormParams p) {
     ln_rows4<kCpl, 32>(h, gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
         if (row < p.rows) store_out<kNt>(o, y + c);
     });
+}
+
+// E4M3 LayerNorm for widths 256 kCpl, two rows per wave (32 lanes per row).
+template <int kCpl, bool kNt>
+__global__ __launch_bounds__(256) void layer_norm_r2_e4m3_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t r = row < p.rows ? row : p.rows - 1;  // rows past the end repeat the last (not stored)
+    const int j = lane & 31;
+    const f16x8v* x = (const f16x8v*)((const _Float16*)p.x + r * p.ldx);
+    const f16x8v* g = (const f16x8v*)p.gamma;
+    const f16x8v* bt = (const f16x8v*)p.beta;
+    f16x8v h[kCpl], gg[kCpl], bb[kCpl];
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i) {
+        h[i] = x[j + 32 * i];
+        gg[i] = g[j + 32 * i];
+        bb[i] = bt[j + 32 * i];
+    }
+    u32x2* y = (u32x2*)((uint8_t*)p.y + r * p.ldy);
+    const float scale = ln_rows4_e4m3<kCpl, 32>(h, gg, bb, p.eps, [&](int, int c, u32x2 codes) __attribute__((always_inline)) {
+        if (row < p.rows) store_out<kNt>(codes, y + c);
+    });
+    if (row < p.rows && j == 0) p.y_scale[row] = scale;
 }
 
 // E4M3 LayerNorm (codes + per-row scales) for widths 128 kCpl, four rows per
@@ -1562,6 +1588,21 @@ hipError_t launch_layer_norm(const LayerNormParams& params_in, hipStream_t strea
         break;
             SDXL_LNR2(3) SDXL_LNR2(4) SDXL_LNR2(5)
 #undef SDXL_LNR2
+        }
+        return hipGetLastError();
+    }
+    if (e4m3 && p.width % 256 == 0 && p.width > 640 && p.width <= 1280 && p.ldx % 8 == 0 &&
+        ((uintptr_t)p.x & 15) == 0 && ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 &&
+        p.ldy % 8 == 0 && ((uintptr_t)p.y & 7) == 0) {
+        const dim3 g8((unsigned)((p.rows + 7) / 8));
+        switch (p.width / 256) {
+#define SDXL_LNR2E(n)                                                                               \
+    case n:                                                                                         \
+        if (nt) hipLaunchKernelGGL((layer_norm_r2_e4m3_kernel<n, true>), g8, block, 0, stream, p);  \
+        else hipLaunchKernelGGL((layer_norm_r2_e4m3_kernel<n, false>), g8, block, 0, stream, p);    \
+        break;
+            SDXL_LNR2E(3) SDXL_LNR2E(4) SDXL_LNR2E(5)
+#undef SDXL_LNR2E
         }
         return hipGetLastError();
     }
