@@ -63,6 +63,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 typedef __attribute__((address_space(3))) i16x8 lds_i16x8;
@@ -168,6 +169,8 @@ __device__ __forceinline__ void lds_dma16(const char* base, uint32_t voff, uint3
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0070); }  // vmcnt(0)
 
 __device__ __forceinline__ void wait_vmem4() { __builtin_amdgcn_s_waitcnt(0x0074); }     // vmcnt(4)
+
+__device__ __forceinline__ void wait_vmem2() { __builtin_amdgcn_s_waitcnt(0x0072); }     // vmcnt(2)
 
 // Output store: non-temporal (streams to memory instead of staying in L2)
 // for large outputs, else ordinary. A compile-time choice: with a run-time
@@ -1218,6 +1221,267 @@ hipError_t launch_short_keys(FusedAttentionParams p, int compute_units, hipStrea
     return hipGetLastError();
 }
 
+
+// ---- short key sequences, 16-row blocks (v_mfma_f32_16x16x32). The same
+// algorithm as short_keys_attention_d64_kernel with half the query rows per
+// wave block: a block's dependent chain (scores, maximum, exponentials, PV,
+// output) is about half as long and there are twice as many blocks, for
+// calls whose 32-row blocks would leave most SIMDs without a wave (CLIP's
+// 77-token self-attention: 72 blocks).
+// Per block and 16-key tile t (kTiles = ceil(k_seq / 16)): S^T tile = K_t Q^T
+// (two MFMAs over d = 64); lane l holds query l & 15 and keys
+// 16t + 4(l >> 4) + i, i < 4, in s[t][i]. O^T = V^T P^T runs over pairs of
+// tiles (32 keys per MFMA; the probability operand of lane group g is keys
+// 4g..4g+3 of the first tile and of the second, so the V^T operand is two
+// transposing LDS reads of those key rows); an odd last tile takes a step
+// whose second half has zero probabilities. Keys past k_seq get a -inf
+// accumulator seed in the last tile. Visibility per key: key < k_seq, key mask, causal (key <= query);
+// a row with no visible key is 0 (reference
+// src/cuda/flash_attention_sm80.cu:214-219).
+template <bool IsBf16>
+__device__ __forceinline__ f32x4 mfma16x32(i16x8 a, i16x8 b, f32x4 c) {
+    if constexpr (IsBf16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// Workgroups per CU: LDS is 4 kTiles + 8 KiB per workgroup.
+constexpr int short16_occupancy(int tiles) { return tiles <= 5 ? 5 : 4; }
+
+template <bool IsBf16, int kTiles, bool kMasked, int kWaves, bool kNt>
+__global__ __launch_bounds__(kWaves * 64, short16_occupancy(kTiles)) void short_keys16_attention_d64_kernel(FusedAttentionParams p) {
+    constexpr int kRows = 16 * kTiles;
+    constexpr int kPerWave = 4 * kTiles / kWaves;  // 1-KiB K/V transfers per wave
+    constexpr int kBlockBytes = 16 * kRowBytes;
+    __shared__ __attribute__((aligned(16))) char kbuf[kRows * kRowBytes];
+    __shared__ __attribute__((aligned(16))) char vbuf[kRows * kRowBytes];
+    __shared__ __attribute__((aligned(16))) char qobuf[kWaves * kBlockBytes];  // per-wave Q / O staging
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;   // lane group: keys 4g..4g+3 of each tile
+    const int r16 = lane & 15; // query row of the block
+    int task;
+    {
+        const int n = p.total_blocks, id = (int)blockIdx.x;
+        const int xcd = id & 7, slot = id >> 3, per = n >> 3, extra = n & 7;
+        task = xcd * per + (xcd < extra ? xcd : extra) + slot;
+    }
+    const int bh = task / p.short_chunks;
+    const int blk_begin = (task % p.short_chunks) * p.short_chunk_blocks;
+    const int blk_end = min(blk_begin + p.short_chunk_blocks, p.q_blocks);
+    const int h = bh % p.heads;
+    const int b = bh / p.heads;
+    const int64_t elem = 2;
+    const char* qbase = (const char*)p.q + ((int64_t)b * p.q_seq * p.q_row_stride + (int64_t)h * kHeadDim) * elem;
+    const char* kbase = (const char*)p.k + ((int64_t)b * p.k_seq * p.k_row_stride + (int64_t)h * kHeadDim) * elem;
+    const char* vbase = (const char*)p.v + ((int64_t)b * p.k_seq * p.v_row_stride + (int64_t)h * kHeadDim) * elem;
+    char* obase = (char*)p.o + ((int64_t)b * p.q_seq * p.o_row_stride + (int64_t)h * kHeadDim) * elem;
+
+    // K/V rows into LDS (swizzled 128-byte rows); rows past k_seq re-read the
+    // last key and are never visible.
+#pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {
+        const int n = wave * kPerWave + j;
+        const bool is_v = n >= 2 * kTiles;
+        const int r8 = is_v ? n - 2 * kTiles : n;
+        const int row = 8 * r8 + (lane >> 3);
+        const int key = min(row, p.k_seq - 1);
+        const uint32_t stride = (uint32_t)((is_v ? p.v_row_stride : p.k_row_stride) * elem);
+        const uint32_t off = __umul24((uint32_t)key, stride) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+        lds_dma16(is_v ? vbase : kbase, off, lds_addr((is_v ? vbuf : kbuf) + 8 * r8 * kRowBytes));
+    }
+
+    // Q rows by DMA into the wave's staging buffer (two 1-KiB transfers per
+    // block); rows past q_seq re-read the last row and are never stored. A
+    // wave's blocks are blk_begin + wave + kWaves i, i < n_mine.
+    char* const wbuf = qobuf + wave * kBlockBytes;
+    const int first = blk_begin + wave;
+    const int n_mine = first < blk_end ? (blk_end - first + kWaves - 1) / kWaves : 0;
+    const uint32_t q_stride_b = (uint32_t)(p.q_row_stride * elem);
+    auto issue_q = [&](int i) __attribute__((always_inline)) {
+        const int blk = first + kWaves * i;
+        const char* src = qbase + (int64_t)(16 * blk) * p.q_row_stride * elem;
+        const int last = p.q_seq - 1 - 16 * blk;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            const uint32_t off = __umul24((uint32_t)min(row, last), q_stride_b) + (uint32_t)(((lane & 7) ^ swz(row)) << 4);
+            lds_dma16(src, off, lds_addr(wbuf + 8 * j * kRowBytes));
+        }
+    };
+    if (n_mine > 0) issue_q(0);
+    uint64_t vis_word[2] = {~0ull, ~0ull};
+    if constexpr (kMasked) {
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const int key = 64 * w + lane;
+            const bool ok = key < p.k_seq && (p.key_mask == nullptr || p.key_mask[(int64_t)b * p.k_seq + key] != 0);
+            vis_word[w] = __builtin_amdgcn_ballot_w64(ok);
+        }
+    }
+    // K and V landed (block 0's two Q transfers, issued after them, may fly)
+    if (n_mine > 0) wait_vmem2();
+    else wait_vmem_all();
+    __syncthreads();
+
+    const int k_swz = swz(r16);
+    int v_off[4];  // transposing V reads: key row 4g + (r16 >> 2), dims 16dt + 4(r16 & 3)
+    {
+        const int row = 4 * g + (r16 >> 2);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            v_off[dt] = row * kRowBytes + (((2 * dt + ((r16 & 3) >> 1)) ^ swz(row)) << 4) + ((r16 & 1) << 3);
+    }
+    const float c = p.scale_log2;
+    f32x4 seed_last;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) seed_last[i] = 16 * (kTiles - 1) + 4 * g + i < p.k_seq ? 0.0f : -__builtin_inff();
+
+    for (int i = 0; i < n_mine; ++i) {
+        const int blk = first + kWaves * i;
+        const int my_query = 16 * blk + r16;
+        // Block i's transfers were issued before block i - 1's 2 stores.
+        if (i == 0) wait_vmem_all();
+        else wait_vmem2();
+        i16x8 qop[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) qop[ks] = *(const lds_i16x8*)(wbuf + r16 * kRowBytes + (((4 * ks + g) ^ k_swz) << 4));
+        auto k_operand = [&](int t, int ks) __attribute__((always_inline)) {
+            return *(const lds_i16x8*)(kbuf + (16 * t + r16) * kRowBytes + (((4 * ks + g) ^ k_swz) << 4));
+        };
+        f32x4 s[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            s[t] = mfma16x32<IsBf16>(k_operand(t, 0), qop[0], t == kTiles - 1 ? seed_last : z);
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) s[t] = mfma16x32<IsBf16>(k_operand(t, 1), qop[1], s[t]);
+        if constexpr (kMasked) {
+            const int causal_lim = p.causal ? my_query - 4 * g : 0x7FFFFFFF;
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) {
+                const uint32_t lane_vis = (uint32_t)(vis_word[t >> 2] >> (16 * (t & 3) + 4 * g));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool ok = ((lane_vis >> e) & 1u) && 16 * t + e <= causal_lim;
+                    s[t][e] = ok ? s[t][e] : -__builtin_inff();
+                }
+            }
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, s[t][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = xhalf_max(mx);
+        const float neg_cm = mx == -__builtin_inff() ? 0.0f : -c * mx;
+
+        f32x4 out[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) out[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        float l = 0.0f;
+        uint32_t pk[kTiles][2];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            float e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) e[u] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][u], c, neg_cm));
+            l += (e[0] + e[1]) + (e[2] + e[3]);
+            pk[t][0] = pack2<IsBf16>(e[0], e[1]);
+            pk[t][1] = pack2<IsBf16>(e[2], e[3]);
+        }
+#pragma unroll
+        for (int ss = 0; ss < kTiles / 2; ++ss) {
+            const i16x8 pop = __builtin_bit_cast(i16x8, u32x4{pk[2 * ss][0], pk[2 * ss][1], pk[2 * ss + 1][0], pk[2 * ss + 1][1]});
+            const char* base = vbuf + 32 * ss * kRowBytes;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt]));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + 16 * kRowBytes + v_off[dt]));
+                out[dt] = mfma16x32<IsBf16>(i16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]}, pop, out[dt]);
+            }
+        }
+        if constexpr (kTiles % 2 == 1) {
+            // odd last tile: a 32-key step whose second half has zero
+            // probabilities (the V operand repeats the tile's rows, finite)
+            const i16x8 pop = __builtin_bit_cast(i16x8, u32x4{pk[kTiles - 1][0], pk[kTiles - 1][1], 0u, 0u});
+            const char* base = vbuf + 16 * (kTiles - 1) * kRowBytes;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(base + v_off[dt]));
+                out[dt] = mfma16x32<IsBf16>(i16x8{lo[0], lo[1], lo[2], lo[3], lo[0], lo[1], lo[2], lo[3]}, pop, out[dt]);
+            }
+        }
+        l += __shfl_xor(l, 16, 64);
+        const float l_tot = xhalf_sum(l);
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        // O rows through the staging buffer: lane holds dims 16dt + 4g .. +3
+        // of row r16 (half g & 1 of chunk 2dt + (g >> 1)).
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const uint32_t w0 = pack2<IsBf16>(out[dt][0] * inv, out[dt][1] * inv);
+            const uint32_t w1 = pack2<IsBf16>(out[dt][2] * inv, out[dt][3] * inv);
+            *(lds_u32x2*)(wbuf + r16 * kRowBytes + (((2 * dt + (g >> 1)) ^ k_swz) << 4) + 8 * (g & 1)) = u32x2{w0, w1};
+        }
+        u32x4 orow[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            orow[j] = *(const lds_u32x4*)(wbuf + row * kRowBytes + (((lane & 7) ^ swz(row)) << 4));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (i + 1 < n_mine) issue_q(i + 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = 8 * j + (lane >> 3);
+            if (16 * blk + row < p.q_seq)
+                store_out<kNt>(orow[j], (u32x4*)(obase + (int64_t)(16 * blk + row) * p.o_row_stride * elem + 16 * (lane & 7)));
+        }
+    }
+}
+
+template <bool IsBf16, bool kMasked>
+hipError_t launch_short_keys16(FusedAttentionParams p, int compute_units, hipStream_t stream) {
+    constexpr int kWaves = 4;
+    const int tiles = (p.k_seq + 15) / 16;
+    const int per_cu = short16_occupancy(tiles);
+    p.q_blocks = (p.q_seq + 15) / 16;
+    const int64_t heads_total = (int64_t)p.heads * p.batch;
+    const int64_t all_blocks = (int64_t)p.q_blocks * heads_total;
+    const int64_t target_wgs = (int64_t)(compute_units > 0 ? compute_units : 256) * per_cu;
+    int64_t chunk = (all_blocks + target_wgs - 1) / target_wgs;
+    chunk = (chunk + kWaves - 1) / kWaves * kWaves;
+    chunk = chunk > p.q_blocks ? p.q_blocks : chunk;
+    p.short_chunk_blocks = (int32_t)chunk;
+    p.short_chunks = (int32_t)((p.q_blocks + chunk - 1) / chunk);
+    const int64_t grid_size = heads_total * p.short_chunks;
+    if (grid_size > INT32_MAX) return hipErrorInvalidValue;
+    p.total_blocks = (int32_t)grid_size;
+    const dim3 grid(p.total_blocks), block(64 * kWaves);
+    const bool nt = (int64_t)p.batch * p.q_seq * p.heads * kHeadDim * 2 >= kStreamOutBytes;
+#define SDXL_SK16_LAUNCH(T)                                                                                          \
+    do {                                                                                                             \
+        if (nt) hipLaunchKernelGGL((short_keys16_attention_d64_kernel<IsBf16, T, kMasked, kWaves, true>), grid, block, 0, stream, p); \
+        else hipLaunchKernelGGL((short_keys16_attention_d64_kernel<IsBf16, T, kMasked, kWaves, false>), grid, block, 0, stream, p); \
+    } while (0)
+    switch (tiles) {
+    case 1: SDXL_SK16_LAUNCH(1); break;
+    case 2: SDXL_SK16_LAUNCH(2); break;
+    case 3: SDXL_SK16_LAUNCH(3); break;
+    case 4: SDXL_SK16_LAUNCH(4); break;
+    case 5: SDXL_SK16_LAUNCH(5); break;
+    case 6: SDXL_SK16_LAUNCH(6); break;
+    case 7: SDXL_SK16_LAUNCH(7); break;
+    default: SDXL_SK16_LAUNCH(8); break;
+    }
+#undef SDXL_SK16_LAUNCH
+    return hipGetLastError();
+}
+
 }  // namespace
 
 int fused_attention_block_queries() { return 32 * kFusedWaves; }
@@ -1231,6 +1495,15 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
     if (p.total_blocks == 0) return hipSuccess;
     if (p.k_seq > 0 && p.k_seq <= kShortKeysMax) {
         const bool masked = p.causal || p.key_mask != nullptr;
+        // Grids of at most 1.5 32-row blocks per CU run 16-row blocks (twice
+        // the waves in flight): CLIP's [2,12,77,77] 4.65 -> 3.56 us,
+        // [2,20,256,77] 3.65 -> 3.27 us; from [2,20,512,77] (2.5 per CU) the
+        // 32-row kernel is as fast or faster (3.86 vs 3.97 us).
+        const int64_t blocks32 = (int64_t)((p.q_seq + 31) / 32) * p.heads * p.batch;
+        if (compute_units > 0 && 2 * blocks32 <= 3 * (int64_t)compute_units) {
+            if (is_bf16) return masked ? launch_short_keys16<true, true>(p, compute_units, stream) : launch_short_keys16<true, false>(p, compute_units, stream);
+            return masked ? launch_short_keys16<false, true>(p, compute_units, stream) : launch_short_keys16<false, false>(p, compute_units, stream);
+        }
         if (is_bf16) return masked ? launch_short_keys<true, true>(p, compute_units, stream) : launch_short_keys<true, false>(p, compute_units, stream);
         return masked ? launch_short_keys<false, true>(p, compute_units, stream) : launch_short_keys<false, false>(p, compute_units, stream);
     }

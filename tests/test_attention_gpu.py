@@ -387,12 +387,18 @@ def test_key_split_workgroups(B, Sq, Sk, H):
 
 
 # ---------------------------------------------------------------- short key sequences (k_seq <= 128)
-# One-pass kernel with K/V wholly in LDS: the 77-token cross-attention and CLIP's causal
-# self-attention (src/cuda/text_encoder.cpp:83, 77 tokens).
+# One-pass kernels with K/V wholly in LDS: the 77-token cross-attention and CLIP's causal
+# self-attention (src/cuda/text_encoder.cpp:83, 77 tokens). Calls of at most 1.5 32-row query
+# blocks per CU (384 on the MI355X's 256 CUs) run 16-row blocks, larger ones 32-row blocks:
+# "small" grids below take the first kernel, "large" ones (800 blocks) the second.
+SHORT_GRIDS = {"small": (2, 200, 3), "large": (2, 640, 20)}
 
+
+@pytest.mark.parametrize("grid", list(SHORT_GRIDS))
 @pytest.mark.parametrize("sk", [1, 2, 16, 17, 31, 32, 33, 48, 49, 64, 77, 80, 81, 96, 112, 127, 128])
-def test_short_keys_lengths(sk):
-    _check_config(2, 200, sk, 3, seed=900 + sk)
+def test_short_keys_lengths(sk, grid):
+    B, Sq, H = SHORT_GRIDS[grid]
+    _check_config(B, Sq, sk, H, seed=900 + sk)
 
 
 @pytest.mark.parametrize("sq", [8192, 8190])
@@ -402,12 +408,14 @@ def test_short_keys_several_blocks_per_wave(sq):
     _check_config(2, sq, 77, 10, seed=950 + sq % 7)
 
 
+@pytest.mark.parametrize("heads", [2, 160])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("sk", [77, 128])
-def test_short_keys_mask_and_causal(causal, sk):
-    B, H = 2, 2
+def test_short_keys_mask_and_causal(causal, sk, heads):
+    """2 heads: the 16-row kernel; 160 heads (3-4 blocks each, 960-1280 in all): the 32-row one."""
+    B, H = 2, heads
     sq = sk  # causal self-attention over the token sequence, as in the text encoder
-    qb, kb, vb = seeded(910, B, sq, 128), seeded(911, B, sk, 128), seeded(912, B, sk, 128)
+    qb, kb, vb = seeded(910, B, sq, 64 * H), seeded(911, B, sk, 64 * H), seeded(912, B, sk, 64 * H)
     mask = (np.random.default_rng(5).random((B, sk)) > 0.3).astype(np.int32)
     mask[1, :] = 0
     got = run(qb, kb, vb, H, causal=causal, key_mask=torch.from_numpy(mask).to(DEV))
@@ -423,8 +431,9 @@ def test_short_keys_clip_causal():
     assert_parity(got, oracle.attention_f16(qb, kb, vb, 12, causal=True), label="clip causal")
 
 
-def test_short_keys_bf16_and_strides():
-    B, S, Sk, H = 2, 300, 77, 2
+@pytest.mark.parametrize("H", [2, 40])
+def test_short_keys_bf16_and_strides(H):
+    B, S, Sk = 2, 300, 77
     W = H * 64
     qb = oracle.normal_f16(930, (B, S, W))
     kvb = oracle.normal_f16(931, (B, Sk, 2 * W))
@@ -435,10 +444,11 @@ def test_short_keys_bf16_and_strides():
     assert_parity(from_dev(out), ref, label="short strided")
 
 
-def test_short_keys_bf16():
-    B, S, Sk, H = 2, 256, 77, 2
-    qf = oracle.normal_f32(940, (B, S, 128))
-    kf, vf = (oracle.normal_f32(941 + i, (B, Sk, 128)) for i in range(2))
+@pytest.mark.parametrize("H", [2, 40])
+def test_short_keys_bf16(H):
+    B, S, Sk = 2, 256, 77
+    qf = oracle.normal_f32(940, (B, S, 64 * H))
+    kf, vf = (oracle.normal_f32(941 + i, (B, Sk, 64 * H)) for i in range(2))
     to_bf = lambda x: torch.from_numpy(x).to(DEV).to(torch.bfloat16)
     qd, kd, vd = to_bf(qf), to_bf(kf), to_bf(vf)
     got = from_dev(sh.attention(qd, kd, vd, H))
@@ -611,9 +621,10 @@ def test_large_logits_masked_first_group(causal):
     assert_parity_f16_out(got, ref, label=f"anchor masked causal={causal}")
 
 
-def test_large_logits_short_keys():
-    """The one-pass 77-key kernel at the same logit range (exact maximum, no anchor)."""
-    B, Sq, Sk, H = 2, 1024, 77, 20
+@pytest.mark.parametrize("B,Sq,Sk,H", [(2, 1024, 77, 20), (1, 256, 77, 4)])
+def test_large_logits_short_keys(B, Sq, Sk, H):
+    """The one-pass 77-key kernels (32-row and 16-row blocks) at the same logit range (exact
+    maximum, no anchor)."""
     qb = oracle.normal_f16(1400, (B, Sq, H * 64), 16.0)
     kb, vb = oracle.normal_f16(1401, (B, Sk, H * 64)), oracle.normal_f16(1402, (B, Sk, H * 64))
     got = run(qb, kb, vb, H)
