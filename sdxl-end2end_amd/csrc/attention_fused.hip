@@ -1486,6 +1486,10 @@ hipError_t launch_short_keys16(FusedAttentionParams p, int compute_units, hipStr
 
 int fused_attention_block_queries() { return 32 * kFusedWaves; }
 
+bool short_keys_16_row_blocks(int64_t blocks32, int compute_units) {
+    return compute_units > 0 && 2 * blocks32 <= 3 * (int64_t)compute_units;
+}
+
 hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, bool is_bf16, int compute_units,
                                       hipStream_t stream) {
     FusedAttentionParams p = params_in;
@@ -1499,8 +1503,7 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
         // the waves in flight): CLIP's [2,12,77,77] 4.65 -> 3.56 us,
         // [2,20,256,77] 3.65 -> 3.27 us; from [2,20,512,77] (2.5 per CU) the
         // 32-row kernel is as fast or faster (3.86 vs 3.97 us).
-        const int64_t blocks32 = (int64_t)((p.q_seq + 31) / 32) * p.heads * p.batch;
-        if (compute_units > 0 && 2 * blocks32 <= 3 * (int64_t)compute_units) {
+        if (short_keys_16_row_blocks((int64_t)((p.q_seq + 31) / 32) * p.heads * p.batch, compute_units)) {
             if (is_bf16) return masked ? launch_short_keys16<true, true>(p, compute_units, stream) : launch_short_keys16<true, false>(p, compute_units, stream);
             return masked ? launch_short_keys16<false, true>(p, compute_units, stream) : launch_short_keys16<false, false>(p, compute_units, stream);
         }

@@ -48,6 +48,9 @@ struct FusedAttentionParams {
 hipError_t launch_fused_attention_d64(const FusedAttentionParams& params, bool is_bf16, int compute_units,
                                       hipStream_t stream);
 int fused_attention_block_queries();
+// Whether a short-key call (k_seq <= kShortKeysMax) with blocks32 32-row query
+// blocks in all runs on 16-row blocks (at most 1.5 32-row blocks per CU).
+bool short_keys_16_row_blocks(int64_t blocks32, int compute_units);
 
 struct OnlineAttentionParams {
     const void* q;

@@ -1476,6 +1476,10 @@ bool q_cross_attention_supported(const LinearParams& p, bool w_fp8, int compute_
     const int64_t tasks = p.m > 0 ? (int64_t)(p.m / 64) * (p.n / 128) : 0;
     if (compute_units <= 0 || tasks > (int64_t)q_cross_attention_per_cu(w_fp8, p.a_scale != nullptr) * compute_units)
         return false;
+    // the fused form computes the attention as the 32-row short-key kernel
+    // does; calls that the attention dispatch gives 16-row blocks stay
+    // separate, so that both forms give the same bits
+    if (p.m <= 0 || short_keys_16_row_blocks((int64_t)(p.m / 32) * (p.n / 64), compute_units)) return false;
     return p.m > 0 && p.seq > 0 && p.seq % 64 == 0 && p.m % p.seq == 0 && p.n % 128 == 0 && p.k % kBK == 0 &&
            p.ctx_len >= 65 && p.ctx_len <= 80 && p.kv != nullptr && p.bias == nullptr && p.residual == nullptr &&
            p.ldkv >= 2 * (int64_t)p.n && p.ldkv % 8 == 0 && ((uintptr_t)p.kv & 15) == 0 && p.ldc % 8 == 0 &&

@@ -491,7 +491,8 @@ def _torch_fp32_cross(x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out, H
 
 # The library's backend choice (AUTO) runs the query projection and the attention as one launch
 # when seq % 64 == 0, W % 128 == 0, 65 <= ctx_len <= 80 and the grid of 64 x 128 tiles is
-# resident at once (three per CU with E4M3 weights and fp16 activations, else two); each wave
+# resident at once (three per CU with E4M3 weights and fp16 activations, else two) and the
+# attention has more than 1.5 32-row query blocks per CU (fewer run on 16-row blocks); each wave
 # attends with the 32 x 64 query block it projected, and the output equals the composition of the
 # individual calls bit for bit. Other shapes, and explicit backends, run the composition itself.
 @pytest.mark.parametrize("B,S,H,fp8,w8,ctx_len", [
@@ -499,8 +500,9 @@ def _torch_fp32_cross(x, gamma, beta, ctx, w_kv, w_q, w_q_scale, w_out, b_out, H
     (2, 1024, 20, True, True, 77),    # level 2, fused, E4M3 weights and activations
     (2, 4096, 10, False, True, 77),   # level 1, fused (640 tiles, three per CU), E4M3 weights
     (2, 4096, 10, True, True, 77),    # level 1, E4M3 activations: 640 tiles > two per CU, composition
-    (1, 128, 2, False, True, 65),     # fused, one key in the last group
-    (1, 192, 4, False, False, 80),    # fused, 16 keys in the last group
+    (1, 4096, 4, False, True, 65),    # fused, one key in the last group
+    (1, 4160, 4, False, False, 80),   # fused, 16 keys in the last group
+    (1, 128, 2, False, True, 65),     # few query blocks: the attention takes 16-row blocks, composition
     (1, 300, 2, False, False, 77),    # S % 64 != 0: composition
     (1, 256, 2, False, False, 64),    # 64 keys: composition
 ])
