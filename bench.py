@@ -44,7 +44,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -105,6 +105,19 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     kernel_ms = start.elapsed_time(end) / steps
     return wall_ms, kernel_ms, out
+
+
+def bench_clip(torch, sh, steps=20, warmup=2):
+    """CLIP-L text encoder self-attention (reference src/cuda/text_encoder.cpp:83): [2, 12, 77, 77]
+    fp16, causal; 72 32-row query blocks, so the library runs it on the 16-row short-key kernel."""
+    B, S, H = 2, 77, 12
+    q, k, v = make_inputs(torch, B, S, S, H, 98)
+    out = torch.empty_like(q)
+    k_ms = time_fn(torch, lambda: sh.attention(q, k, v, H, causal=True, out=out), steps, warmup)
+    by = sh.attention_bytes(B, H, S, S)
+    return {"shape": [B, H, S, S, 64], "what": "CLIP-L causal self-attention, 16-row short-key kernel",
+            "kernel_us": round(k_ms * 1e3, 2), "kernel_timing": "HIP graph replay",
+            "hbm_gbs": round(by / (k_ms * 1e-3) / 1e9, 1)}
 
 
 def time_fn(torch, fn, steps, warmup, reps=10):
@@ -450,6 +463,9 @@ def main():
             fn()
         torch.cuda.synchronize()
         return
+    if args.only == "clip":
+        print(json.dumps(bench_clip(torch, sh, args.steps, args.warmup)), flush=True)
+        return
     if args.only:
         B, Sq, Sk, H, _ = configs[args.only]
         q, k, v = make_inputs(torch, B, Sq, Sk, H, 1)
@@ -519,6 +535,7 @@ def main():
                 sec[name]["measured_hbm_gbs"] = round(t / (k_ms * 1e-3) / 1e9, 1)
                 sec[name]["measured_hbm_frac"] = round(t / (k_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
             del qq, kk, vv
+        sec["clip_causal"] = bench_clip(torch, sh)
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
         sec["l2_self_sublayer"] = bench_sublayer(torch, sh, B=2, S=1024, H=20)
         sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
