@@ -456,6 +456,32 @@ def test_short_keys_bf16(H):
     assert_parity(got, ref, max_abs=1e-2, mean_abs=1e-3, label="short bf16")
 
 
+@pytest.mark.parametrize("heads", [2, 160])
+def test_short_keys_bf16_mask_and_causal(heads):
+    """bf16 CLIP-shaped causal self-attention with a key mask, on both short-key kernels (2 heads:
+    16-row blocks; 160 heads: 32-row blocks), against the fp32 oracle on the bf16 values."""
+    B, S = 2, 77
+    qf = oracle.normal_f32(960, (B, S, 64 * heads))
+    kf, vf = (oracle.normal_f32(961 + i, (B, S, 64 * heads)) for i in range(2))
+    mask = (np.random.default_rng(7).random((B, S)) > 0.3).astype(np.int32)
+    to_bf = lambda x: torch.from_numpy(x).to(DEV).to(torch.bfloat16)
+    qd, kd, vd = to_bf(qf), to_bf(kf), to_bf(vf)
+    got = from_dev(sh.attention(qd, kd, vd, heads, causal=True, key_mask=torch.from_numpy(mask).to(DEV)))
+    ref = oracle.attention_f32(qd.float().cpu().numpy(), kd.float().cpu().numpy(), vd.float().cpu().numpy(), heads,
+                               key_mask=mask, causal=True, threads=THREADS)
+    # bf16: the output's rounding is up to 2^-8 |ref| (half an ulp at 8 significant bits) and the
+    # probabilities' rounding to bf16 before P.V up to 2^-9 sum_j p_j |v_j| (the oracle on |V|);
+    # causal rows with one or two visible keys return V values of magnitude up to ~5
+    ref_absv = oracle.attention_f32(qd.float().cpu().numpy(), kd.float().cpu().numpy(),
+                                    np.abs(vd.float().cpu().numpy()), heads, key_mask=mask, causal=True,
+                                    threads=THREADS)
+    err = np.abs(got - ref)
+    bound = 2.0 ** -8 * np.abs(ref) + 2.0 ** -9 * ref_absv + 2e-3
+    assert np.isfinite(got).all()
+    assert (err <= bound).all(), ("short bf16 mask causal", heads, float((err - bound).max()))
+    assert err.mean() <= 1e-3, err.mean()
+
+
 # ---------------------------------------------------------------- mixed 12-wave workgroups
 # Unmasked, non-causal calls with Sk % 64 == 0 whose 32-row blocks fill rounds of 10-block
 # workgroups within 10 % of an even share per CU (T blocks, r rounds: r * 10 <= 1.1 * T / 256 on the
