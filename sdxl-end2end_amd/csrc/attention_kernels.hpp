@@ -37,7 +37,7 @@ struct FusedAttentionParams {
     float inv_scale_log2;  // 1 / scale_log2 (finite)
     int32_t whole_units;   // filled by the launcher: 128-row workgroups (ids first)
     int32_t split_units;   // filled by the launcher: 64-row key-split workgroups
-    int32_t short_chunk_blocks;  // filled by the short-key launcher: 32-row blocks per workgroup
+    int32_t short_chunk_blocks;  // filled by the short-key launchers: query blocks (32 or 16 rows) per workgroup
     int32_t short_chunks;        // filled by the short-key launcher: workgroups per (batch, head)
     int32_t mixed_total;         // filled by the launcher: 32-row blocks of the call (mixed kind)
     int32_t mixed_wgs;           // filled by the launcher: mixed workgroups
