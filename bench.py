@@ -44,7 +44,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,torch_sdpa,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -105,6 +105,43 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     kernel_ms = start.elapsed_time(end) / steps
     return wall_ms, kernel_ms, out
+
+
+def bench_torch_sdpa(torch, steps=50, reps=5):
+    """For comparison only (not this library): PyTorch's own scaled_dot_product_attention on the
+    same box, per backend, on the c3 / c1 / c2 shapes as [B, H, S, 64] fp16 contiguous tensors, scale
+    1/8; device us per call from events around `steps` eager calls, best of `reps`."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    res = {}
+    for name, (B, H, S, Sk) in {"c3": (2, 10, 4096, 4096), "c1": (2, 20, 1024, 1024), "c2": (2, 20, 1024, 77)}.items():
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(5)
+        q = torch.randn(B, H, S, 64, device="cuda:0", generator=g).half()
+        k = torch.randn(B, H, Sk, 64, device="cuda:0", generator=g).half()
+        v = torch.randn(B, H, Sk, 64, device="cuda:0", generator=g).half()
+        fl = 4.0 * B * H * S * Sk * 64
+        for be in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+            try:
+                with sdpa_kernel(be):
+                    fn = lambda: F.scaled_dot_product_attention(q, k, v, scale=0.125)
+                    for _ in range(10):
+                        fn()
+                    torch.cuda.synchronize()
+                    best = float("inf")
+                    for _ in range(reps):
+                        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                        e0.record()
+                        for _ in range(steps):
+                            fn()
+                        e1.record()
+                        torch.cuda.synchronize()
+                        best = min(best, e0.elapsed_time(e1) / steps * 1e3)
+                res[f"{name}_{be.name.lower()}"] = {"shape": [B, H, S, Sk, 64], "us": round(best, 2),
+                                                    "tflops": round(fl / (best * 1e-6) / 1e12, 1)}
+            except RuntimeError as e:
+                res[f"{name}_{be.name.lower()}"] = {"unavailable": str(e)[:120]}
+    return {"what": f"torch {torch.__version__} scaled_dot_product_attention (comparison only)", "results": res}
 
 
 def bench_clip(torch, sh, steps=20, warmup=2):
@@ -463,6 +500,9 @@ def main():
             fn()
         torch.cuda.synchronize()
         return
+    if args.only == "torch_sdpa":
+        print(json.dumps(bench_torch_sdpa(torch)), flush=True)
+        return
     if args.only == "clip":
         print(json.dumps(bench_clip(torch, sh, args.steps, args.warmup)), flush=True)
         return
@@ -540,6 +580,7 @@ def main():
         sec["l2_self_sublayer"] = bench_sublayer(torch, sh, B=2, S=1024, H=20)
         sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
         sec["vae_mid_attention_fp32"] = bench_vae_attention(torch, sh)
+        sec["torch_sdpa_comparison"] = bench_torch_sdpa(torch)
         result["secondary"] = sec
 
     if not args.no_cpu:
