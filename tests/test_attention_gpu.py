@@ -666,3 +666,66 @@ def test_tiny_scale_is_uniform_softmax(scale):
     got = run(qb, kb, vb, 2, scale=scale)
     mean_v = oracle.f16_bits_to_f32(vb).astype(np.float64).mean(axis=1, keepdims=True)
     assert np.abs(got - mean_v).max() <= 1e-3
+
+
+# ---------------------------------------------------------------- random shapes
+# Seeded random calls over every kernel the dispatch can pick (short-key 16- and 32-row, 4-wave
+# whole / key-split, 64-KiB, mixed 12-wave, causal / key mask, fp16 / bf16), each checked
+# elementwise against torch fp32 attention on the same device values. Bound per element: one ulp
+# of the output type at |ref| (2^-10 |ref| fp16, 2^-8 bf16), the rounding of the probabilities
+# before P.V (2^-11 resp. 2^-8 of sum_j p_j |v_j|, torch on |V|) and the 2e-3 bar.
+
+def _torch_attention_f32(q, k, v, heads, causal, mask, abs_v=False):
+    torch = pytest.importorskip("torch")
+    B, Sq, W = q.shape
+    Sk = k.shape[1]
+    qh = q.float().view(B, Sq, heads, 64).transpose(1, 2)
+    kh = k.float().view(B, Sk, heads, 64).transpose(1, 2)
+    vh = v.float().view(B, Sk, heads, 64).transpose(1, 2)
+    if abs_v:
+        vh = vh.abs()
+    s = qh @ kh.transpose(-1, -2) / 8.0
+    vis = torch.ones(B, 1, Sq, Sk, dtype=torch.bool, device=q.device)
+    if causal:
+        vis = vis & torch.ones(Sq, Sk, dtype=torch.bool, device=q.device).tril()
+    if mask is not None:
+        vis = vis & (mask[:, None, None, :] != 0)
+    p = torch.softmax(s.masked_fill(~vis, float("-inf")), -1).nan_to_num(0.0)
+    return (p @ vh).transpose(1, 2).reshape(B, Sq, W)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_shapes_vs_torch_fp32(seed):
+    import random
+    import torch
+    rng = random.Random(1000 + seed)
+    done = 0
+    while done < 60:
+        short = rng.random() < 0.5
+        B, H = rng.randint(1, 4), rng.choice([1, 2, 3, 5, 8, 10, 12, 20, 24])
+        Sq = rng.choice([rng.randint(1, 300), rng.randint(1, 2500)])
+        Sk = rng.randint(1, 128) if short else rng.choice([rng.randint(1, 300), rng.randint(1, 2500),
+                                                           64 * rng.randint(1, 40)])
+        if B * H * Sq * Sk > 20e6:
+            continue
+        dt = rng.choice([torch.float16, torch.bfloat16])
+        mode = rng.choice(["plain", "plain", "causal", "mask", "both"])
+        g = torch.Generator(device=DEV).manual_seed(seed * 1000 + done)
+        q = torch.randn(B, Sq, H * 64, device=DEV, generator=g).to(dt)
+        k = torch.randn(B, Sk, H * 64, device=DEV, generator=g).to(dt)
+        v = torch.randn(B, Sk, H * 64, device=DEV, generator=g).to(dt)
+        mask = (torch.rand(B, Sk, device=DEV, generator=g) > 0.3).int() if mode in ("mask", "both") else None
+        causal = mode in ("causal", "both")
+        label = f"B{B} Sq{Sq} Sk{Sk} H{H} {dt} {mode}"
+        print(label, flush=True)
+        got = sh.attention(q, k, v, H, causal=causal, key_mask=mask).float()
+        ref = _torch_attention_f32(q, k, v, H, causal, mask)
+        ref_abs = _torch_attention_f32(q, k, v, H, causal, mask, abs_v=True)
+        if dt == torch.float16:
+            bound = 2.0 ** -10 * ref.abs() + 2.0 ** -11 * ref_abs + 2e-3
+        else:
+            bound = 2.0 ** -8 * ref.abs() + 2.0 ** -8 * ref_abs + 2e-3
+        assert bool(torch.isfinite(got).all()), label
+        excess = float(((got - ref).abs() - bound).max())
+        assert excess <= 0.0, (label, excess)
+        done += 1
