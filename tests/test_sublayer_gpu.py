@@ -546,3 +546,78 @@ def test_cross_sublayer_matches_composition_and_fp32(B, S, H, fp8, w8, ctx_len):
     sh.cross_attn_sublayer(xi, gamma, beta, w_q, w_q_scale, kv, w_out, b_out, H, out=xi, fp8_activations=fp8)
     torch.cuda.synchronize()
     assert torch.equal(xi, y)
+
+
+# ---------------------------------------------------------------- random shapes
+# Seeded random calls of the projection (fp16 or E4M3 weights; bias, residual), the LayerNorm and
+# the LayerNorm inside the E4M3 projection (fp16 or E4M3 activations), each checked elementwise
+# against torch fp32 on the same device values (E4M3 codes decoded by torch's float8_e4m3fn):
+# one fp16 ulp at |ref| plus the accumulation's rounding (2^-16 of sum |a||w|; for the LayerNorm
+# projection the normalised rows' fp16 rounding, 2^-10 of sum |ln||w|, or their E4M3 rounding,
+# 2^-4), and the fused forms bit-equal to their two-launch compositions.
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_projection_and_layer_norm_shapes(seed):
+    import random
+    rng = random.Random(2000 + seed)
+    for n in range(40):
+        kind = rng.choice(["lin16", "lin8", "ln", "lnlin", "lnlin8"])
+        M = rng.choice([rng.randint(1, 300), rng.randint(1, 5000)])
+        g = torch.Generator(device="cuda").manual_seed(seed * 1000 + n)
+        if kind in ("lin16", "lin8"):
+            K, N = 64 * rng.randint(1, 24), 4 * rng.randint(1, 768)
+            a = torch.randn(M, K, device="cuda", generator=g).half()
+            w = (torch.randn(N, K, device="cuda", generator=g) * 0.05).half()
+            bias = torch.randn(N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
+            res = torch.randn(M, N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
+            label = f"{kind} M{M} N{N} K{K} bias={bias is not None} residual={res is not None}"
+            print(label, flush=True)
+            if kind == "lin8":
+                wq, ws = sh.quantize_e4m3_rows(w)
+                wf = wq.view(torch.float8_e4m3fn).float() * ws[:, None]
+                got = sh.linear(a, wq, w_scale=ws, bias=bias, residual=res)
+            else:
+                wf = w.float()
+                got = sh.linear(a, w, bias=bias, residual=res)
+            ref = a.float() @ wf.T
+            if bias is not None:
+                ref = ref + bias.float()
+            if res is not None:
+                ref = ref + res.float()
+            bound = 2.0 ** -10 * ref.abs() + 2.0 ** -16 * (a.float().abs() @ wf.abs().T) + 1e-5
+        elif kind == "ln":
+            W = 2 * rng.randint(1, 1024)
+            x = (torch.randn(M, W, device="cuda", generator=g) * rng.choice([1, 5]) + rng.choice([0, 3])).half()
+            gm = torch.randn(W, device="cuda", generator=g).half()
+            bt = torch.randn(W, device="cuda", generator=g).half()
+            label = f"ln M{M} W{W}"
+            print(label, flush=True)
+            got = sh.layer_norm(x, gm, bt)
+            ref = torch.nn.functional.layer_norm(x.float(), (W,), gm.float(), bt.float(), 1e-5)
+            bound = 2.0 ** -10 * ref.abs() + 2e-3 * gm.float().abs() + 1e-4
+        else:
+            K, N = 640, 128 * rng.randint(1, 16)
+            x = torch.randn(M, K, device="cuda", generator=g).half()
+            gm = (1 + 0.1 * torch.randn(K, device="cuda", generator=g)).half()
+            bt = (0.1 * torch.randn(K, device="cuda", generator=g)).half()
+            wq, ws = sh.quantize_e4m3_rows((torch.randn(N, K, device="cuda", generator=g) * 0.05).half())
+            bias = torch.randn(N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
+            fp8 = kind == "lnlin8"
+            label = f"{kind} M{M} N{N} bias={bias is not None}"
+            print(label, flush=True)
+            got = sh.layer_norm_linear(x, gm, bt, wq, ws, bias=bias, fp8_activations=fp8)
+            if fp8:
+                codes, cs = sh.layer_norm_e4m3(x, gm, bt)
+                comp = sh.linear_e4m3(codes, cs, wq, ws, bias=bias)
+            else:
+                comp = sh.linear(sh.layer_norm(x, gm, bt), wq, w_scale=ws, bias=bias)
+            torch.cuda.synchronize()
+            assert torch.equal(got, comp), label
+            ln = torch.nn.functional.layer_norm(x.float(), (K,), gm.float(), bt.float(), 1e-5)
+            wf = wq.view(torch.float8_e4m3fn).float() * ws[:, None]
+            ref = ln @ wf.T + (bias.float() if bias is not None else 0.0)
+            bound = 2.0 ** -10 * ref.abs() + (2.0 ** -4 if fp8 else 2.0 ** -10) * (ln.abs() @ wf.abs().T) + 1e-4
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(got.float()).all()), label
+        excess = float(((got.float() - ref).abs() - bound).max())
+        assert excess <= 0.0, (label, excess)
