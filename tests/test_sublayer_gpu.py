@@ -621,3 +621,58 @@ def test_random_projection_and_layer_norm_shapes(seed):
         assert bool(torch.isfinite(got.float()).all()), label
         excess = float(((got.float() - ref).abs() - bound).max())
         assert excess <= 0.0, (label, excess)
+
+
+@pytest.mark.parametrize("seed", range(2))
+def test_random_sublayers_equal_their_compositions(seed):
+    """Seeded random self- and cross-attention sublayers (fp16 or E4M3 weights, fp16 or E4M3
+    activations, LayerNorm fusion on or off, 1-128 context tokens, ragged sequence lengths): the one
+    call equals the composition of the individual calls bit for bit, whichever fused forms the
+    library picks."""
+    import random
+    rng = random.Random(3000 + seed)
+    done = 0
+    while done < 25:
+        cross = rng.random() < 0.5
+        B, H = rng.randint(1, 2), rng.choice([1, 2, 4, 5, 10, 20])
+        W = 64 * H
+        S = rng.choice([rng.randint(1, 300), rng.randint(1, 4096), 64 * rng.randint(1, 64)])
+        if B * S * W > 12e6:
+            continue
+        w8 = rng.random() < 0.7
+        fp8 = w8 and rng.random() < 0.4
+        g = torch.Generator(device="cuda").manual_seed(seed * 1000 + done)
+        x = torch.randn(B, S, W, device="cuda", generator=g).half()
+        gm = (1 + 0.1 * torch.randn(W, device="cuda", generator=g)).half()
+        bt = (0.1 * torch.randn(W, device="cuda", generator=g)).half()
+        w_out = (torch.randn(W, W, device="cuda", generator=g) * 0.02).half()
+        b_out = (torch.randn(W, device="cuda", generator=g) * 0.02).half()
+        n_in = W if cross else 3 * W
+        w_in = (torch.randn(n_in, W, device="cuda", generator=g) * 0.02).half()
+        wq, ws = sh.quantize_e4m3_rows(w_in) if w8 else (w_in, None)
+        if cross:
+            L, C = rng.randint(1, 128), rng.choice([768, 1280, 2048])
+            ctx = torch.randn(B, L, C, device="cuda", generator=g).half()
+            kv = sh.project_context_kv(ctx, (torch.randn(2 * W, C, device="cuda", generator=g) * 0.02).half())
+            label = f"cross B{B} S{S} H{H} L{L} w8={w8} fp8={fp8}"
+            print(label, flush=True)
+            y = sh.cross_attn_sublayer(x, gm, bt, wq, ws, kv, w_out, b_out, H, fp8_activations=fp8)
+        else:
+            lnf = rng.random() < 0.5
+            label = f"self B{B} S{S} H{H} w8={w8} fp8={fp8} ln_fusion={lnf}"
+            print(label, flush=True)
+            y = sh.attn_sublayer(x, gm, bt, wq, ws, w_out, b_out, H, fp8_activations=fp8, ln_fusion=lnf)
+        if fp8:
+            codes, cs = sh.layer_norm_e4m3(x, gm, bt)
+            proj = sh.linear_e4m3(codes.view(-1, W), cs, wq, ws)
+        else:
+            proj = sh.linear(sh.layer_norm(x, gm, bt).view(-1, W), wq, w_scale=ws)
+        if cross:
+            attn = sh.attention(proj.view(B, S, W), kv[..., :W], kv[..., W:], H)
+        else:
+            qkv = proj.view(B, S, 3 * W)
+            attn = sh.attention(qkv[..., :W], qkv[..., W:2 * W], qkv[..., 2 * W:], H)
+        y2 = sh.linear(attn.view(-1, W), w_out, bias=b_out, residual=x.view(-1, W)).view(B, S, W)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2), label
+        done += 1
