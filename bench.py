@@ -6,7 +6,8 @@ self-attention, fp16 Q,K,V [2, 10, 4096, 64] (configs[2]; BSHD storage
 [2, 4096, 640]), through the C ABI (sdxl_attn_fwd, backend auto -> flash-gfx950).
 
 One "step" = one sdxl_attn_fwd call over the whole [2, 10, 4096, 4096] problem,
-inputs resident in HBM. Timing: W untimed warm-up calls, then K calls bracketed
+inputs resident in HBM. Timing: W untimed warm-up calls and a 200-ms untimed clock-settle
+phase (reported as settle_ms, settle_launches), then K calls bracketed
 by torch.cuda.synchronize(); a HIP event pair on the launch stream around the same
 K launches gives the average launch duration for the roofline figure.
 
@@ -32,6 +33,8 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_FP8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
+# untimed clock-settle phase before every timed region of time_calls (ms of wall time)
+SETTLE_MS = 200.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fused_attention_c3_traffic.txt")
 CROSS_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "short_keys_attention_cross_traffic.txt")
 
@@ -80,8 +83,13 @@ def check_output(out, bits, heads, rows=((0, 16), (2040, 2056), (4080, 4096))):
             "pass": worst <= 2e-3 and total / n <= 2e-4}
 
 
-def time_calls(torch, sh, q, k, v, heads, steps, warmup):
-    """Returns (ms per step over the timed region, mean launch ms from HIP events, output).
+def time_calls(torch, sh, q, k, v, heads, steps, warmup, settle_ms=SETTLE_MS):
+    """Returns (ms per step over the timed region, mean launch ms from HIP events, output, settle).
+
+    Before the timed region: `warmup` untimed calls, then a clock-settle phase of untimed calls
+    for at least `settle_ms` of wall time (batches of launches, synchronised between batches).
+    The device clock ramps over the first few dozen launches of a process; a few warm-up calls
+    alone leave the timed region on a rising clock. `settle` reports the phase (ms, launches).
 
     The timed region is `steps` back-to-back calls bracketed by torch.cuda.synchronize(); one
     HIP event pair on the launch stream (the current stream, which sdxl_hip.attention launches
@@ -92,6 +100,13 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     for _ in range(warmup):
         sh.attention(q, k, v, heads, out=out)
     torch.cuda.synchronize()
+    n_settle, t_settle = 0, time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < settle_ms:
+        for _ in range(20):
+            sh.attention(q, k, v, heads, out=out)
+        n_settle += 20
+        torch.cuda.synchronize()
+    settle = {"settle_ms": round((time.perf_counter() - t_settle) * 1e3, 1), "settle_launches": n_settle}
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -104,7 +119,7 @@ def time_calls(torch, sh, q, k, v, heads, steps, warmup):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     kernel_ms = start.elapsed_time(end) / steps
-    return wall_ms, kernel_ms, out
+    return wall_ms, kernel_ms, out, settle
 
 
 def bench_torch_sdpa(torch, steps=50, reps=5):
@@ -517,7 +532,7 @@ def main():
     desc = sh.make_desc(B, Sq, Sk, H)
     backend = sh.load().sdxl_attn_kernel_name(sh.resolve_backend(desc)).decode()
     torch.cuda.synchronize()
-    wall_ms, kernel_ms, out = time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
+    wall_ms, kernel_ms, out, settle = time_calls(torch, sh, q, k, v, H, args.steps, args.warmup)
     parity = check_output(out, bits, H)
     flops = sh.attention_flops(B, H, Sq, Sk)
     value = flops / (wall_ms * 1e-3) / 1e12
@@ -530,6 +545,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": settle["settle_ms"],
+        "settle_launches": settle["settle_launches"],
         "ms_per_step": round(wall_ms, 5),
         "us_per_call": round(wall_ms * 1e3, 2),
         "higher_is_better": True,
@@ -557,7 +574,7 @@ def main():
             if name == "c3":
                 continue
             qq, kk, vv = make_inputs(torch, b, sq, sk, h, 99)
-            w_ms, _, oo = time_calls(torch, sh, qq, kk, vv, h, 100, 10)
+            w_ms, _, oo, _ = time_calls(torch, sh, qq, kk, vv, h, 100, 10, settle_ms=50.0)
             # device time per call from captured-graph replays: the per-launch host cost of the
             # ctypes call (~6 us) would otherwise dominate these short kernels
             k_ms = time_fn(torch, lambda: sh.attention(qq, kk, vv, h, out=oo), 20, 2)

@@ -97,12 +97,16 @@ public:
     void trim_memory_arena() const;
 
     // HIP graph capture of Ops calls (reference runtime.hpp:153-157). Between
-    // begin and end, allocations are served from the cache when a block of the
-    // size is there (after a warm-up pass: no driver call inside the capture),
-    // else by hipMalloc; every block allocated in this window is held when its
-    // tensor is freed instead of re-entering the cache, because replays of the
-    // captured graph keep writing it. release_graph_allocations() returns the
-    // held blocks to the cache once the graphs that use them are destroyed.
+    // begin and end, allocations must be served from the cache (run the
+    // sequence once eagerly first): a size with no cached block throws
+    // HipError, since no driver allocation can be recorded into the capture.
+    // Every block allocated in this window, and every block freed in it (a
+    // graph input whose tensor dies inside the captured sequence), is held
+    // when its tensor is freed instead of re-entering the cache, because
+    // replays of the captured graph keep reading and writing it.
+    // release_graph_allocations() returns the held blocks to the cache once
+    // the graphs that use them are destroyed. Outside a capture, a hipMalloc
+    // that runs out of memory frees the cached blocks and retries once.
     void begin_graph_allocation_capture() const;
     void end_graph_allocation_capture() const noexcept;
     void release_graph_allocations() const;

@@ -169,6 +169,9 @@ Tensor Ops::layer_norm_linear(const Tensor& input, const Tensor& norm_weight, co
                                                   weight.data(), weight.dequant_scale_data(),
                                                   bias ? bias->data() : nullptr, output.data(), runtime_->stream());
     runtime_->end_profile(scope);
+    // the fused kernel's alignment and stride conditions are checked by the call itself (nothing is
+    // launched when it declines): fall back to the two-launch composition, the same values
+    if (st == SDXL_STATUS_UNSUPPORTED) return linear(layer_norm(input, norm_weight, norm_bias, epsilon), weight, bias);
     check(st);
     return output;
 }

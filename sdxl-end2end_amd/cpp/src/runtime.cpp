@@ -7,6 +7,7 @@
 #include <map>
 #include <mutex>
 #include <sstream>
+#include <string>
 #include <unordered_map>
 #include <unordered_set>
 
@@ -57,8 +58,23 @@ struct DeviceArena {
             stats.cached_bytes -= bytes;
             ++stats.cache_hits;
         } else {
+            // A driver allocation cannot be recorded into a stream capture: inside the
+            // capture window every block must come from the cache.
+            if (capturing)
+                throw HipError("device arena: no cached block of " + std::to_string(bytes) +
+                               " bytes inside a HIP graph capture window (run the captured sequence once "
+                               "eagerly first, so that its blocks are cached)");
             SDXL_HIP_CHECK(hipSetDevice(device));
-            SDXL_HIP_CHECK(hipMalloc(&p, bytes));
+            hipError_t status = hipMalloc(&p, bytes);
+            if (status == hipErrorOutOfMemory && !free_blocks.empty()) {
+                // cached blocks of other sizes hold the memory: return them to the driver, retry once
+                (void)hipGetLastError();
+                for (auto& [size, q] : free_blocks) (void)hipFree(q);
+                free_blocks.clear();
+                stats.cached_bytes = 0;
+                status = hipMalloc(&p, bytes);
+            }
+            SDXL_HIP_CHECK(status);
             ++stats.driver_allocations;
         }
         stats.live_bytes += bytes;
@@ -70,7 +86,11 @@ struct DeviceArena {
     void give_back(void* p, std::size_t bytes) noexcept {
         std::lock_guard<std::mutex> lock(mu);
         stats.live_bytes -= bytes;
-        if (capture_blocks.erase(p) != 0) {
+        // Held for captured graphs: blocks allocated inside a capture window (replays
+        // write them), and every block freed inside one, wherever it was allocated (a
+        // graph input whose tensor dies during the captured sequence, x = f(x), is still
+        // read by replays). Nothing is freed to the driver or re-cached meanwhile.
+        if (capture_blocks.erase(p) != 0 || capturing) {
             graph_held.emplace_back(p, bytes);
             stats.graph_held_bytes += bytes;
             return;

@@ -273,6 +273,55 @@ void graph_capture_cases() {
     require(released.graph_held_bytes == 0, "held blocks released");
     runtime.trim_memory_arena();
     require(runtime.memory_arena_stats().cached_bytes == 0, "trim frees the cache");
+
+    // x = f(x) inside the capture: the input tensor x (allocated before the capture) dies inside
+    // the captured sequence. Its block must stay out of the cache while the graph exists, or the
+    // next eager tensor of that size would take it and replays would read that tensor as x.
+    {
+        Tensor x = Tensor::from_host_f32(runtime, qh);
+        const auto x_eager = ops.attention(x, k, v, 2).to_host_f32(runtime);  // warm-up: the output size is cached
+        runtime.begin_graph_allocation_capture();
+        hipGraph_t g2 = nullptr;
+        SDXL_HIP_CHECK(hipStreamBeginCapture(runtime.stream(), hipStreamCaptureModeGlobal));
+        Tensor y = ops.attention(x, k, v, 2);
+        x = Tensor();  // the input's last reference dies inside the capture
+        SDXL_HIP_CHECK(hipStreamEndCapture(runtime.stream(), &g2));
+        runtime.end_graph_allocation_capture();
+        const auto other_host = filled({2, 256, 128}, [](std::size_t i) { return std::cos(static_cast<float>(i) * 0.29F); });
+        const Tensor other = Tensor::from_host_f32(runtime, other_host);  // same size as x, allocated eagerly
+        const auto other_before = other.to_host_f32(runtime);
+        hipGraphExec_t exec2 = nullptr;
+        SDXL_HIP_CHECK(hipGraphInstantiate(&exec2, g2, nullptr, nullptr, 0));
+        for (int replay = 0; replay < 3; ++replay) {
+            SDXL_HIP_CHECK(hipGraphLaunch(exec2, runtime.stream()));
+            const auto got = y.to_host_f32(runtime);
+            for (std::size_t i = 0; i < got.values.size(); ++i)
+                require(std::memcmp(&got.values[i], &x_eager.values[i], sizeof(float)) == 0,
+                        "replay reads the freed input, not the eager tensor of its size");
+            const auto other_now = other.to_host_f32(runtime);
+            for (std::size_t i = 0; i < other_now.values.size(); ++i)
+                require(std::memcmp(&other_now.values[i], &other_before.values[i], sizeof(float)) == 0,
+                        "eager tensor intact across replays");
+        }
+        SDXL_HIP_CHECK(hipGraphExecDestroy(exec2));
+        SDXL_HIP_CHECK(hipGraphDestroy(g2));
+        y = Tensor();
+        runtime.release_graph_allocations();
+        require(runtime.memory_arena_stats().graph_held_bytes == 0, "held blocks released");
+    }
+
+    // a size with no cached block inside a capture window: a clear error, no driver allocation
+    {
+        runtime.begin_graph_allocation_capture();
+        bool threw = false;
+        try {
+            (void)runtime.allocate_device(123457);
+        } catch (const HipError&) {
+            threw = true;
+        }
+        runtime.end_graph_allocation_capture();
+        require(threw, "cache miss inside a capture window throws");
+    }
     std::cout << "graph capture cases passed\n";
 }
 
