@@ -47,7 +47,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,torch_sdpa,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,torch_sdpa,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8,l2_outproj,l1_outproj,l2_qkv,l2_ln) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -257,7 +257,7 @@ def bench_sublayer(torch, sh, steps=50, warmup=5, B=2, S=4096, H=10):
             e["tflops"] = round(fl / (ms * 1e-3) / 1e12, 1)
             e["mfma_frac"] = round(fl / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
         out["stages"][name] = e
-    if W == 640:
+    if W in (640, 1280):
         # LayerNorm inside the q|k|v projection (sdxl_layer_norm_linear): replaces the first two stages
         fl, by = sh.linear_flops(M, 3 * W, W), 2.0 * M * W + 3 * W * W + 2.0 * M * 3 * W
         t = time_fn(torch, lambda: sh.layer_norm_linear(x.view(M, W), gamma, beta, q8, s8, out=qkv), steps, warmup)
@@ -279,7 +279,7 @@ def bench_sublayer(torch, sh, steps=50, warmup=5, B=2, S=4096, H=10):
             e["tflops"] = round(fl / (t * 1e-3) / 1e12, 1)
             e["fp8_mfma_frac"] = round(fl / (t * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4)
         out["fp8_activations"][name] = e
-    if W == 640:
+    if W in (640, 1280):
         # E4M3 LayerNorm inside the fp8 projection (sdxl_layer_norm_linear_e4m3): replaces the two stages above
         fl, by = sh.linear_flops(M, 3 * W, W), 2.0 * M * W + 3 * W * W + 2.0 * M * 3 * W
         t = time_fn(torch, lambda: sh.layer_norm_linear(x.view(M, W), gamma, beta, q8, s8, out=qkv,
@@ -511,6 +511,34 @@ def main():
             codes, cs = sh.layer_norm_e4m3(a.view(1, M, W), torch.ones(W, dtype=torch.float16, device="cuda:0"),
                                            torch.zeros(W, dtype=torch.float16, device="cuda:0"))
             fn = lambda: sh.linear_e4m3(codes.view(M, W), cs, q8, s8, out=out)
+        for _ in range(args.warmup + args.steps):
+            fn()
+        torch.cuda.synchronize()
+        return
+    if args.only in ("l2_outproj", "l1_outproj", "l2_qkv", "l2_ln"):
+        # profiling aid: one sublayer stage alone, eager launches. l2_outproj: the level-2 output
+        # projection [2048, 1280] x [1280, 1280]^T fp16 + bias + residual (l1_outproj: [8192, 640]
+        # x [640, 640]^T); l2_qkv: the level-2 q|k|v projection with E4M3 weights [3840, 1280];
+        # l2_ln: the level-2 LayerNorm rows [2048, 1280]
+        M, W = (8192, 640) if args.only == "l1_outproj" else (2048, 1280)
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(7)
+        a = torch.randn(M, W, device="cuda:0", generator=g).half()
+        if args.only == "l2_qkv":
+            q8, s8 = sh.quantize_e4m3_rows((torch.randn(3 * W, W, device="cuda:0", generator=g) * 0.02).half())
+            out = torch.empty(M, 3 * W, dtype=torch.float16, device="cuda:0")
+            fn = lambda: sh.linear(a, q8, w_scale=s8, out=out)
+        elif args.only == "l2_ln":
+            gamma = torch.ones(W, dtype=torch.float16, device="cuda:0")
+            beta = torch.zeros(W, dtype=torch.float16, device="cuda:0")
+            out = torch.empty(1, M, W, dtype=torch.float16, device="cuda:0")
+            fn = lambda: sh.layer_norm(a.view(1, M, W), gamma, beta, out=out)
+        else:
+            w = (torch.randn(W, W, device="cuda:0", generator=g) * 0.02).half()
+            bias = (torch.randn(W, device="cuda:0", generator=g) * 0.02).half()
+            res = torch.randn(M, W, device="cuda:0", generator=g).half()
+            out = torch.empty(M, W, dtype=torch.float16, device="cuda:0")
+            fn = lambda: sh.linear(a, w, bias=bias, residual=res, out=out)
         for _ in range(args.warmup + args.steps):
             fn()
         torch.cuda.synchronize()

@@ -93,7 +93,7 @@ sdxl_status sdxl_quantize_e4m3_rows(int64_t rows, int64_t cols, const void* w, u
  * sdxl_linear, so c equals sdxl_layer_norm followed by sdxl_linear bit for bit;
  * the normalised rows never reach HBM. desc as sdxl_linear (k = width, a_row_stride
  * = x row stride; w_dtype must be SDXL_DTYPE_E4M3; residual_row_stride 0). eps 0
- * means 1e-5. SDXL_STATUS_UNSUPPORTED unless k == 640, n % 128 == 0, 16-byte
+ * means 1e-5. SDXL_STATUS_UNSUPPORTED unless k == 640 or k == 1280, n % 128 == 0, 16-byte
  * aligned x rows, gamma, beta and w rows, 8-byte aligned c rows. */
 sdxl_status sdxl_layer_norm_linear(const sdxl_linear_desc* desc, const void* x, const void* gamma,
                                    const void* beta, float eps, const void* w, const float* w_scale,
@@ -123,7 +123,9 @@ typedef struct sdxl_sublayer_desc {
     int32_t qkv_activations;
     /* 0: the LayerNorm runs inside the q|k|v projection (sdxl_layer_norm_linear, or
      * sdxl_layer_norm_linear_e4m3 with E4M3 activations) where that kernel takes the
-     * shape (E4M3 w_qkv, width 640), else as its own launch; 1: always its own
+     * shape (E4M3 w_qkv, width 640 or 1280) and is the faster choice (at most two
+     * workgroups per 64-row block: the level-1 blocks, not the level-2 ones), else
+     * as its own launch; 1: always its own
      * launch. Same results either way. */
     int32_t ln_fusion;
 } sdxl_sublayer_desc;

@@ -40,8 +40,9 @@ public:
 
     // linear(layer_norm(input, norm_weight, norm_bias, epsilon), weight, bias) — the
     // transformer block's norm -> projection (unet.cpp:106-112) — in one launch where the
-    // fused kernel takes the shape (Float8E4M3 weight, width 640, N % 128 == 0: the
-    // level-1 q|k|v), else as the two calls; the same result either way.
+    // fused kernel takes the shape and is faster (Float8E4M3 weight, width 640, N % 128 == 0:
+    // the level-1 q|k|v; at width 1280 the two launches are faster), else as the two calls;
+    // the same result either way.
     [[nodiscard]] Tensor layer_norm_linear(const Tensor& input, const Tensor& norm_weight, const Tensor& norm_bias,
                                            const Tensor& weight, const Tensor* bias = nullptr,
                                            float epsilon = 1.0e-5F) const;

@@ -1059,33 +1059,41 @@ __global__ __launch_bounds__(256) void layer_norm_v8_kernel(LayerNormParams p) {
 }
 
 // LayerNorm fused into the projection that consumes it, for K = kK input
-// features and E4M3 weights (the transformer block's norm1 -> q|k|v at level 1,
-// src/cuda/unet.cpp:106-112): c[m, n] = w_scale[n] * sum_k LN(x)[m, k] w[n, k]
-// (+ bias[n]), with LN(x) exactly as the LayerNorm kernel rounds it to fp16.
+// features (640: level 1, 1280: level 2) and E4M3 weights (the transformer
+// block's norm1 -> q|k|v and norm2 -> q, src/cuda/unet.cpp:106-112,120-124):
+// c[m, n] = w_scale[n] * sum_k LN(x)[m, k] w[n, k] (+ bias[n]), with LN(x)
+// exactly as the standalone LayerNorm kernel of that width rounds it.
 //
 // One workgroup of 8 waves per CU (two per SIMD) owns 64 rows and a range of
-// 128-column chunks of the output. Prologue: the rows are normalised once
-// (four rows per wave, ln_rows4: the standalone LayerNorm kernel's code) into
-// LDS, then each wave takes its 32 rows' normalised values into registers as
-// MFMA operands (kK / 16 steps of 8 values: 160 VGPRs at kK = 640), so the
-// activations never go back to HBM and are read from LDS once. kAFp8: the
-// LayerNorm rounds each row to E4M3 codes with a per-row scale (ln_rows4_e4m3,
-// the standalone E4M3 LayerNorm's code; 80 VGPRs of codes) and the projection
-// runs on v_mfma_f32_32x32x64_f8f6f4 with the weight codes as read (no
-// decode), as linear_kernel's fp8 form. Main loop: the E4M3 weight
-// rows of each chunk stream HBM/L2 -> LDS by global_load_lds_dwordx4 in
-// 128-column K stages (two 64-byte-row sub-stages, linear_kernel's layout)
-// through a ring of three (prefetch distance two, one barrier per stage);
-// wave (wm, wn) computes rows 32 wm .. +31 x columns 32 wn .. +31 of a chunk
-// as one chain of kK / 16 v_mfma_f32_32x32x16_f16 over linear_kernel's K
-// order, operand layouts and code decode (fp8: one MFMA per 64-column
-// sub-stage), so the fp32 sums equal that kernel's. A chunk's output is written (LDS-staged, 64-byte row segments)
-// during the next chunk's second stage, so the stores drain under MFMA work
-// instead of in one burst at the end. Per-column scales and bias sit in LDS,
-// and every lane stores (rows past m repeat row m - 1 with its own value), so
-// the vector-memory operations in the loop are a fixed sequence and every
-// wait counts exactly the transfers it needs.
-constexpr int kLnLinMaxCols = 2048;  // output columns per workgroup (scales and bias in LDS)
+// 128-column chunks of the output. Prologue: the rows are normalised once with
+// the standalone LayerNorm's code for the width (640: ln_rows4, four rows per
+// wave-quarter of 16 lanes; 1280: two rows per wave-half of 32 lanes) into LDS,
+// then each wave takes its 32 rows' normalised values into registers as MFMA
+// operands (kK / 16 steps of 8 values: 160 VGPRs at kK = 640), so the
+// activations never go back to HBM. At kK = 1280 with fp16 activations
+// (kSplitA) the registers hold K columns 0-639 and LDS keeps columns 640-1279
+// of all 64 rows for the whole kernel (80 KiB), read per K step in the second
+// half of every chunk. kAFp8: the LayerNorm rounds each row to E4M3 codes with
+// a per-row scale (ln_rows4_e4m3, the standalone E4M3 LayerNorm's code; kK
+// codes per row: 80 VGPRs at 640, 160 at 1280) and the projection runs on
+// v_mfma_f32_32x32x64_f8f6f4 with the weight codes as read (no decode), as
+// linear_kernel's fp8 form. Main loop: the E4M3 weight rows of each chunk
+// stream HBM/L2 -> LDS by global_load_lds_dwordx4 in 128-column K stages (two
+// 64-byte-row sub-stages, linear_kernel's layout) through a ring of three
+// (prefetch distance two, one barrier per stage); wave (wm, wn) computes rows
+// 32 wm .. +31 x columns 32 wn .. +31 of a chunk as one chain of kK / 16
+// v_mfma_f32_32x32x16_f16 over linear_kernel's K order, operand layouts and
+// code decode (fp8: one MFMA per 64-column sub-stage), so the fp32 sums equal
+// that kernel's. At the end of a chunk each wave rounds its 32 x 32 block to
+// fp16 (scale, bias: linear_kernel's epilogue arithmetic) into a 2-KiB LDS
+// staging; the block is stored as 64-byte row segments during the next
+// chunk's second stage, so the stores drain under MFMA work instead of in one
+// burst at the end. Per-column scales and bias sit in LDS, and every lane
+// stores (rows past m repeat row m - 1 with its own value), so the
+// vector-memory operations in the loop are a fixed sequence and every wait
+// counts exactly the transfers it needs.
+template <int kK>
+constexpr int ln_linear_max_cols() { return kK > 640 ? 1024 : 2048; }  // output columns per workgroup
 
 template <int kK, bool kAFp8, bool kNt>
 __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
@@ -1093,13 +1101,23 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     constexpr int kSteps = kK / 16;          // MFMA K steps
     constexpr int kStageBytes = 2 * 128 * 64;  // two sub-stages of 128 code rows x 64 bytes
     constexpr int kRing = 3;
-    constexpr int kARow = kAFp8 ? kK : 2 * kK;  // one normalised row, bytes (fp16 or E4M3 codes)
-    static_assert(kK % 128 == 0, "128-column K stages; the operand swizzle works on groups of 16 chunks");
-    static_assert(8 * 32 * 128 <= 64 * kARow, "epilogue staging fits in the row buffer");
+    constexpr int kLanes = kK > 640 ? 32 : 16;   // lanes per row in the LayerNorm (the standalone kernel's)
+    constexpr int kCpl = kK / (8 * kLanes);      // 16-byte fp16 chunks per lane and row
+    constexpr int kRowsPerGroup = 64 / kLanes;   // rows per wave and LayerNorm call
+    constexpr int kGroups = 8 / kRowsPerGroup;   // LayerNorm calls per wave (8 rows)
+    constexpr bool kSplitA = !kAFp8 && kK > 640;  // K columns 640.. from LDS
+    constexpr int kRegSteps = kSplitA ? 40 : kSteps;  // K steps held in registers (fp16)
+    constexpr int kHalfChunks = 80;               // 16-byte chunks of 640 fp16 columns
+    constexpr int kARow = kAFp8 ? kK : (kSplitA ? 2 * 640 : 2 * kK);  // bytes of one row in abuf
+    constexpr int kMaxCols = ln_linear_max_cols<kK>();
+    constexpr int kStgBytes = 32 * 32 * 2;        // one wave's fp16 32 x 32 staging
+    static_assert(kK % 128 == 0 && kCpl * 8 * kLanes == kK, "width");
+    static_assert(kSplitA || 8 * kStgBytes <= 64 * kARow, "epilogue staging fits in the row buffer");
     __shared__ __attribute__((aligned(16))) char ring[kRing][kStageBytes];
     __shared__ __attribute__((aligned(16))) char abuf[64 * kARow];
-    __shared__ __attribute__((aligned(16))) float sc_lds[kLnLinMaxCols];
-    __shared__ __attribute__((aligned(16))) float bias_lds[kLnLinMaxCols];
+    __shared__ __attribute__((aligned(16))) char stg_own[kSplitA ? 8 * kStgBytes : 16];
+    __shared__ __attribute__((aligned(16))) float sc_lds[kMaxCols];
+    __shared__ __attribute__((aligned(16))) float bias_lds[kMaxCols];
     __shared__ float rs_lds[64];  // E4M3 activations: the rows' scales
 
     const int lane = threadIdx.x & 63;
@@ -1144,7 +1162,7 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     // Per-column scales and bias of the workgroup's columns: loaded now, with
     // the rows below, and written to LDS after the LayerNorm (one memory round
     // trip for both).
-    constexpr int kColsPerThread = kLnLinMaxCols / 512;
+    constexpr int kColsPerThread = kMaxCols / 512;
     float sc_reg[kColsPerThread], bias_reg[kColsPerThread];
     {
         const int n0 = c_begin * 128, ncols = nch * 128;
@@ -1156,43 +1174,57 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
         }
     }
 
-    // ---- LayerNorm of the block's 64 rows (wave w: rows 8 w .. +7 as two groups
-    // of four, ln_rows4: the standalone LayerNorm's arithmetic; rows past m
-    // repeat row m - 1). Row r's 16-byte chunk c sits at slot c ^ (r & 15).
+    // ---- LayerNorm of the block's 64 rows: wave w takes rows 8 w .. +7 as
+    // kGroups calls of the standalone kernel's code (rows past m repeat row
+    // m - 1). fp16 rows: 16-byte chunk c of row r at slot c ^ (r & 15); with
+    // kSplitA, chunks 0-79 (columns 0-639) go to LDS now and chunks 80-159 are
+    // kept in registers until the first half has been taken into operand
+    // registers, then written over it.
+    constexpr int kKeep = kSplitA ? 3 : 1;  // chunks i = 2, 3, 4 of a lane may lie past column 640
+    f16x8v keep[kGroups][kKeep];
     {
-        constexpr int kCpl = kK / 128;
-        const int j = lane & 15;
+        const int j = lane & (kLanes - 1);
         const f16x8v* g = (const f16x8v*)p.gamma;
         const f16x8v* bt = (const f16x8v*)p.beta;
-        f16x8v gg[kCpl], bb[kCpl], h[2][kCpl];
+        f16x8v gg[kCpl], bb[kCpl];
 #pragma unroll
         for (int i = 0; i < kCpl; ++i) {
-            gg[i] = g[j + 16 * i];
-            bb[i] = bt[j + 16 * i];
+            gg[i] = g[j + kLanes * i];
+            bb[i] = bt[j + kLanes * i];
         }
+        // rows loaded two calls at a time (all loads of a pair issued before its first use)
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int gm = min(m0 + 8 * wave + 4 * half + (lane >> 4), p.m - 1);
-            const f16x8v* xr = (const f16x8v*)((const _Float16*)p.x + (int64_t)gm * p.ldx);
+        for (int g2 = 0; g2 < kGroups; g2 += 2) {
+            f16x8v h[2][kCpl];
 #pragma unroll
-            for (int i = 0; i < kCpl; ++i) h[half][i] = xr[j + 16 * i];
-        }
+            for (int u = 0; u < 2; ++u) {
+                const int gm = min(m0 + 8 * wave + kRowsPerGroup * (g2 + u) + lane / kLanes, p.m - 1);
+                const f16x8v* xr = (const f16x8v*)((const _Float16*)p.x + (int64_t)gm * p.ldx);
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int r = 8 * wave + 4 * half + (lane >> 4);
-            if constexpr (kAFp8) {
-                // E4M3 rows (ln_rows4_e4m3, the standalone E4M3 LayerNorm's code):
-                // the 8 codes of fp16 chunk c at byte 8c, 16-byte slots swizzled
-                // by r & 7
-                const float sc = ln_rows4_e4m3<kCpl>(h[half], gg, bb, p.eps,
-                                                     [&](int, int c, u32x2 codes) __attribute__((always_inline)) {
-                    *(lds_u32x2*)(abuf + r * kARow + (((c >> 1) ^ (r & 7)) << 4) + 8 * (c & 1)) = codes;
-                });
-                if ((lane & 15) == 0) rs_lds[r] = sc;
-            } else {
-                ln_rows4<kCpl>(h[half], gg, bb, p.eps, [&](int, int c, f16x8v o) __attribute__((always_inline)) {
-                    *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) = o;
-                });
+                for (int i = 0; i < kCpl; ++i) h[u][i] = xr[j + kLanes * i];
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int grp = g2 + u;
+                const int r = 8 * wave + kRowsPerGroup * grp + lane / kLanes;
+                if constexpr (kAFp8) {
+                    // E4M3 rows (ln_rows4_e4m3, the standalone E4M3 LayerNorm's code):
+                    // the 8 codes of fp16 chunk c at byte 8c, 16-byte slots swizzled
+                    // by r & 7
+                    const float sc = ln_rows4_e4m3<kCpl, kLanes>(h[u], gg, bb, p.eps,
+                                                                 [&](int, int c, u32x2 codes) __attribute__((always_inline)) {
+                        *(lds_u32x2*)(abuf + r * kARow + (((c >> 1) ^ (r & 7)) << 4) + 8 * (c & 1)) = codes;
+                    });
+                    if (j == 0) rs_lds[r] = sc;
+                } else {
+                    ln_rows4<kCpl, kLanes>(h[u], gg, bb, p.eps, [&](int i, int c, f16x8v o) __attribute__((always_inline)) {
+                        if (!kSplitA || c < kHalfChunks)
+                            *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + ((c ^ (r & 15)) << 4)) = o;
+                        if constexpr (kSplitA) {
+                            if (i >= 2) keep[grp][i - 2] = o;
+                        }
+                    });
+                }
             }
         }
     }
@@ -1203,69 +1235,87 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
     }
     __syncthreads();
     // Activation operands of the wave's rows: step ks = 4 s + 2 pp + q (s: 64-column
-    // sub-stage) takes columns 64 s + 32 pp + 16 hf + 8 q .. +7 (linear_kernel's K order).
+    // sub-stage) takes columns 64 s + 32 pp + 16 hf + 8 q .. +7 (linear_kernel's K order),
+    // i.e. 16-byte chunk a_chunk(ks) of the row.
     // E4M3 activations: one fp8 MFMA per 64-column sub-stage s, the lane
     // supplying bytes 64 s + 32 hf .. +31 of its row (linear_kernel's fp8 order).
-    i16x8 aop[kAFp8 ? 1 : kSteps];
+    const int ar = 32 * wm + col;
+    auto a_chunk = [&](int ks) __attribute__((always_inline)) {
+        return 8 * (ks >> 2) + 4 * ((ks >> 1) & 1) + 2 * hf + (ks & 1);
+    };
+    i16x8 aop[kAFp8 ? 1 : kRegSteps];
     i32x8 aop8[kAFp8 ? kK / 64 : 1];
-    {
-        const int ar = 32 * wm + col;
-        if constexpr (kAFp8) {
+    if constexpr (kAFp8) {
 #pragma unroll
-            for (int s8 = 0; s8 < kK / 64; ++s8) {
-                const u32x4 lo = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf) ^ (ar & 7)) << 4));
-                const u32x4 hi = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf + 1) ^ (ar & 7)) << 4));
-                aop8[s8] = __builtin_bit_cast(i32x8, u32x4x2{lo, hi});
-            }
-        } else {
+        for (int s8 = 0; s8 < kK / 64; ++s8) {
+            const u32x4 lo = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf) ^ (ar & 7)) << 4));
+            const u32x4 hi = *(const lds_u32x4*)(abuf + ar * kARow + (((4 * s8 + 2 * hf + 1) ^ (ar & 7)) << 4));
+            aop8[s8] = __builtin_bit_cast(i32x8, u32x4x2{lo, hi});
+        }
+    } else {
 #pragma unroll
-            for (int ks = 0; ks < kSteps; ++ks) {
-                const int c = 8 * (ks >> 2) + 4 * ((ks >> 1) & 1) + 2 * hf + (ks & 1);
-                aop[ks] = *(const lds_i16x8*)(abuf + ar * kARow + ((c ^ (ar & 15)) << 4));
+        for (int ks = 0; ks < kRegSteps; ++ks)
+            aop[ks] = *(const lds_i16x8*)(abuf + ar * kARow + ((a_chunk(ks) ^ (ar & 15)) << 4));
+    }
+    __syncthreads();  // kSplitA: the row buffer takes columns 640-1279; else it becomes the epilogue staging
+    if constexpr (kSplitA) {
+        const int j = lane & (kLanes - 1);
+#pragma unroll
+        for (int grp = 0; grp < kGroups; ++grp) {
+            const int r = 8 * wave + kRowsPerGroup * grp + lane / kLanes;
+#pragma unroll
+            for (int i = 2; i < kCpl; ++i) {
+                const int c = j + kLanes * i;
+                if (c >= kHalfChunks)
+                    *(__attribute__((address_space(3))) f16x8v*)(abuf + r * kARow + (((c - kHalfChunks) ^ (r & 15)) << 4)) =
+                        keep[grp][i - 2];
             }
         }
+        __syncthreads();
     }
-    __syncthreads();  // the row buffer becomes the epilogue staging
+    (void)keep;
 
     const int wr = 32 * wn + col;  // weight row of this lane within a chunk
     const int w_off = wr * 64, w_swz = (wr >> 2) & 3;
     typedef float f32x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
-    char* stg = abuf + wave * (32 * 128);
-    // Epilogue of one chunk's 32 x 32 block, in two parts: park() writes it
-    // row-major to the wave's LDS staging at the end of the chunk (128-byte fp32
-    // rows, chunk c of row r at c ^ (r & 7); acc[4u + q] is row col, column
-    // 8u + 4hf + q), store() reads it back during the next chunk with lane l on
-    // columns 4 (l % 8) .. +3 of rows l / 8 + 8 it, scales, adds the bias,
-    // rounds and stores: exactly four stores per lane.
-    auto park = [&](const f32x16& a) __attribute__((always_inline)) {
+    char* stg = (kSplitA ? stg_own : abuf) + wave * kStgBytes;
+    // Epilogue of one chunk's 32 x 32 block, in two parts: park() at the end of
+    // the chunk forms the outputs ((sum x row scale) then scale and bias in one
+    // fused multiply-add, fp32, then fp16: linear_kernel's epilogue rounding)
+    // and writes them to the wave's staging (64-byte fp16 rows, 8-byte unit v
+    // of row r at v ^ ((r >> 2) & 7): conflict-free in both directions; acc[4u
+    // + q] is row col, column 8u + 4hf + q); store() reads them back during
+    // the next chunk with lane l on columns 4 (l % 8) .. +3 of rows l / 8 + 8 it
+    // and stores: exactly four stores per lane.
+    auto park = [&](const f32x16& a, int ci) __attribute__((always_inline)) {
+        const float rs = kAFp8 ? rs_lds[ar] : 1.0f;
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            *(lds_f32x4*)(stg + col * 128 + (((2 * u + hf) ^ (col & 7)) << 4)) =
-                f32x4{a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3]};
+        for (int u = 0; u < 4; ++u) {
+            const int lc = ci * 128 + 32 * wn + 8 * u + 4 * hf;  // column within the workgroup's range
+            const f32x4 e_scale = *(const lds_f32x4*)(sc_lds + lc);
+            const f32x4 e_bias = *(const lds_f32x4*)(bias_lds + lc);
+            f32x4 v = {a[4 * u], a[4 * u + 1], a[4 * u + 2], a[4 * u + 3]};
+            if constexpr (kAFp8) v = f32x4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
+            // the empty asm keeps the compiler from rounding the fma straight to
+            // fp16 (v_fma_mix)
+            f32x4 o = {__builtin_fmaf(v[0], e_scale[0], e_bias[0]), __builtin_fmaf(v[1], e_scale[1], e_bias[1]),
+                       __builtin_fmaf(v[2], e_scale[2], e_bias[2]), __builtin_fmaf(v[3], e_scale[3], e_bias[3])};
+            asm volatile("" : "+v"(o));
+            const f16x4 h4 = {(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]};
+            *(lds_u32x2*)(stg + col * 64 + (((2 * u + hf) ^ ((col >> 2) & 7)) << 3)) = __builtin_bit_cast(u32x2, h4);
+        }
     };
+    // (32-bit element offsets: m * ldc + n < 2^31, checked on the host)
     auto store = [&](int ci) __attribute__((always_inline)) {
-        const int lc = ci * 128 + 32 * wn + 4 * (lane & 7);  // column within the workgroup's range
-        const f32x4 e_scale = *(const lds_f32x4*)(sc_lds + lc);
-        const f32x4 e_bias = *(const lds_f32x4*)(bias_lds + lc);
-        const int en = c_begin * 128 + lc;
+        const int en = (c_begin + ci) * 128 + 32 * wn + 4 * (lane & 7);
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
             const int r = (lane >> 3) + 8 * it;
             const int m = min(m0 + 32 * wm + r, p.m - 1);
-            f32x4 v = *(const lds_f32x4*)(stg + r * 128 + (((lane & 7) ^ (r & 7)) << 4));
-            if constexpr (kAFp8) {
-                const float rs = rs_lds[32 * wm + r];
-                v = f32x4{v[0] * rs, v[1] * rs, v[2] * rs, v[3] * rs};
-            }
-            // fp32 value first ((sum x row scale) then one fused multiply-add),
-            // then fp16, as linear_kernel's epilogue rounds: the empty asm keeps
-            // the compiler from rounding the fma straight to fp16 (v_fma_mix)
-            f32x4 o = {__builtin_fmaf(v[0], e_scale[0], e_bias[0]), __builtin_fmaf(v[1], e_scale[1], e_bias[1]),
-                       __builtin_fmaf(v[2], e_scale[2], e_bias[2]), __builtin_fmaf(v[3], e_scale[3], e_bias[3])};
-            asm volatile("" : "+v"(o));
-            store_out<kNt>(f16x4{(_Float16)o[0], (_Float16)o[1], (_Float16)o[2], (_Float16)o[3]},
-                           (f16x4*)((_Float16*)p.c + (int64_t)m * p.ldc + en));
+            const u32x2 v = *(const lds_u32x2*)(stg + r * 64 + (((lane & 7) ^ ((r >> 2) & 7)) << 3));
+            const uint32_t off = (uint32_t)m * (uint32_t)p.ldc + (uint32_t)en;
+            store_out<kNt>(__builtin_bit_cast(f16x4, v), (f16x4*)((_Float16*)p.c + off));
         }
     };
 
@@ -1317,19 +1367,32 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
                 }
                 continue;
             }
-            // code reads two pairs ahead of their MFMAs
+            // activation operands of K step ks: registers, or (kSplitA, second
+            // half of the chunk) the LDS rows
+            const bool lds_a = kSplitA && st >= kStages / 2;
+            auto read_a = [&](int ks) __attribute__((always_inline)) -> i16x8 {
+                return *(const lds_i16x8*)(abuf + ar * kARow + (((a_chunk(ks) - kHalfChunks) ^ (ar & 15)) << 4));
+            };
+            // code reads two pairs ahead of their MFMAs; LDS activations (kSplitA,
+            // second half of the chunk) at the pair's start
             u32x4 wq[4];
             wq[0] = read_w(0);
             wq[1] = read_w(1);
 #pragma unroll
             for (int pr = 0; pr < 4; ++pr) {
                 if (pr + 2 < 4) wq[pr + 2] = read_w(pr + 2);
+                i16x8 aq[2];
+                if (lds_a) {
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) aq[q] = read_a(8 * st + 2 * pr + q);
+                }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                     const uint2 lo = e4m3x4_to_f16(wq[pr][2 * q]), hi = e4m3x4_to_f16(wq[pr][2 * q + 1]);
-                    acc = mfma32(__builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y}),
-                                 aop[8 * st + 2 * pr + q], acc);
+                    const int ks = 8 * st + 2 * pr + q;
+                    const i16x8 a_op = lds_a ? aq[q] : aop[ks < kRegSteps ? ks : 0];
+                    acc = mfma32(__builtin_bit_cast(i16x8, u32x4{lo.x, lo.y, hi.x, hi.y}), a_op, acc);
                 }
                 if (st == 1 && pr == 1 && ci > 0) {
                     store(ci - 1);
@@ -1340,7 +1403,7 @@ __global__ __launch_bounds__(512, 1) void ln_linear_kernel(LnLinearParams p) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        park(acc);  // the wave's staging was read back in this chunk's K stage 1
+        park(acc, ci);  // the wave's staging was read back in this chunk's K stage 1
     }
     store(nch - 1);
 }
@@ -1511,36 +1574,56 @@ hipError_t launch_q_cross_attention(const LinearParams& params_in, bool w_fp8, i
 }
 
 bool ln_linear_supported(const LnLinearParams& p) {
-    return p.k == 640 && p.m > 0 && p.n >= 128 && p.n % 128 == 0 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
+    return (p.k == 640 || p.k == 1280) && p.m > 0 && p.n >= 128 && p.n % 128 == 0 && p.ldx % 8 == 0 && ((uintptr_t)p.x & 15) == 0 &&
            ((uintptr_t)p.gamma & 15) == 0 && ((uintptr_t)p.beta & 15) == 0 && p.ldw % 16 == 0 &&
            ((uintptr_t)p.w & 15) == 0 && p.w_scale != nullptr && ((uintptr_t)p.w_scale & 3) == 0 &&
            (p.bias == nullptr || ((uintptr_t)p.bias & 1) == 0) && p.ldc % 4 == 0 && ((uintptr_t)p.c & 7) == 0 &&
-           p.ldw * 128 <= 0x7FFFFFFF;  // 32-bit transfer offsets
+           p.ldw * 128 <= 0x7FFFFFFF &&  // 32-bit transfer offsets
+           (int64_t)(p.m - 1) * p.ldc + p.n <= 0x7FFFFFFF;  // 32-bit output offsets
+}
+
+// Work split of the fused LayerNorm projection: one workgroup per CU (144-152
+// KiB of LDS), row blocks of 64, and the output columns split so that the
+// grid fills the CUs once (at most ln_linear_max_cols columns per workgroup).
+// Every workgroup of a row block normalises its 64 rows.
+static void ln_linear_split(LnLinearParams& p, int compute_units) {
+    const int cus = compute_units > 0 ? compute_units : 256;
+    const int max_cols = p.k > 640 ? ln_linear_max_cols<1280>() : ln_linear_max_cols<640>();
+    p.m_blocks = (p.m + 63) / 64;
+    p.chunks = p.n / 128;
+    const int min_split = (p.chunks * 128 + max_cols - 1) / max_cols;
+    const int fill = p.m_blocks >= cus ? 1 : cus / p.m_blocks;
+    p.n_split = std::min(p.chunks, std::max(min_split, fill));
+}
+
+bool ln_linear_preferred(const LnLinearParams& params, int compute_units) {
+    if (!ln_linear_supported(params)) return false;
+    LnLinearParams p = params;
+    ln_linear_split(p, compute_units);
+    return p.n_split <= 2;
 }
 
 hipError_t launch_ln_linear(const LnLinearParams& params_in, int compute_units, hipStream_t stream) {
     LnLinearParams p = params_in;
     if (!ln_linear_supported(p)) return hipErrorInvalidValue;
-    // One workgroup per CU (140 KiB of LDS): row blocks of 64, and the output
-    // columns split so that the grid fills the CUs once (at most
-    // kLnLinMaxCols columns per workgroup).
-    const int cus = compute_units > 0 ? compute_units : 256;
-    p.m_blocks = (p.m + 63) / 64;
-    p.chunks = p.n / 128;
-    const int min_split = (p.chunks * 128 + kLnLinMaxCols - 1) / kLnLinMaxCols;
-    const int fill = p.m_blocks >= cus ? 1 : cus / p.m_blocks;
-    p.n_split = std::min(p.chunks, std::max(min_split, fill));
+    ln_linear_split(p, compute_units);
     const int64_t tasks = (int64_t)p.m_blocks * p.n_split;
     if (tasks > 0x7FFFFFFF) return hipErrorInvalidValue;
     const dim3 grid((unsigned)tasks), block(512);
     const bool nt = (int64_t)p.m * p.n * 2 >= kStreamOutBytes;
-    if (p.a_fp8) {
-        if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, true, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ln_linear_kernel<640, true, false>), grid, block, 0, stream, p);
-    } else {
-        if (nt) hipLaunchKernelGGL((ln_linear_kernel<640, false, true>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((ln_linear_kernel<640, false, false>), grid, block, 0, stream, p);
-    }
+#define SDXL_LNL(K)                                                                                       \
+    do {                                                                                                  \
+        if (p.a_fp8) {                                                                                    \
+            if (nt) hipLaunchKernelGGL((ln_linear_kernel<K, true, true>), grid, block, 0, stream, p);    \
+            else hipLaunchKernelGGL((ln_linear_kernel<K, true, false>), grid, block, 0, stream, p);      \
+        } else {                                                                                          \
+            if (nt) hipLaunchKernelGGL((ln_linear_kernel<K, false, true>), grid, block, 0, stream, p);   \
+            else hipLaunchKernelGGL((ln_linear_kernel<K, false, false>), grid, block, 0, stream, p);     \
+        }                                                                                                 \
+    } while (0)
+    if (p.k == 640) SDXL_LNL(640);
+    else SDXL_LNL(1280);
+#undef SDXL_LNL
     return hipGetLastError();
 }
 

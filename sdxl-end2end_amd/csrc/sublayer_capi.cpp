@@ -220,7 +220,7 @@ sdxl_status ln_linear_params(const sdxl_linear_desc* d, const void* x, const voi
     p.a_fp8 = a_fp8 ? 1 : 0;
     if (d->m > 0 && d->n > 0 && !sdxl_hip::ln_linear_supported(p))
         return sdxl_hip_fail(SDXL_STATUS_UNSUPPORTED,
-                             "sdxl_layer_norm_linear: needs k == 640, n % 128 == 0, 16-byte aligned x rows, gamma, beta "
+                             "sdxl_layer_norm_linear: needs k == 640 or 1280, n % 128 == 0, 16-byte aligned x rows, gamma, beta "
                              "and w rows, 8-byte aligned c rows");
     return SDXL_STATUS_OK;
 }
@@ -318,7 +318,9 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     qd.w_dtype = d->w_qkv_dtype;
     sdxl_status st;
     // LayerNorm fused into the projection where the kernel takes the shape
-    // (E4M3 weights, width 640: the level-1 blocks); else two launches.
+    // (E4M3 weights, width 640 or 1280) and is the faster choice (the level-1
+    // blocks; not the level-2 ones, whose 2048 rows are normalised again by 8
+    // workgroups per row block); else two launches.
     // (checked quietly: an unsupported shape is no error here)
     sdxl_hip::LnLinearParams lp{};
     lp.x = x;
@@ -337,7 +339,7 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* d, const void* x, const
     lp.a_fp8 = act_fp8 ? 1 : 0;
     const bool fuse = d->ln_fusion == 0 && d->w_qkv_dtype == SDXL_DTYPE_E4M3 && M <= INT32_MAX &&
                       3 * W <= INT32_MAX && x != nullptr && ln_gamma != nullptr && ln_beta != nullptr &&
-                      w_qkv != nullptr && sdxl_hip::ln_linear_supported(lp);
+                      w_qkv != nullptr && sdxl_hip::ln_linear_preferred(lp, compute_units());
     if (fuse) {
         st = launch_status(sdxl_hip::launch_ln_linear(lp, compute_units(), reinterpret_cast<hipStream_t>(stream)),
                            "sdxl_attn_sublayer");

@@ -75,6 +75,11 @@ struct LnLinearParams {
     int32_t m_blocks, n_split, chunks;  // filled by the launcher
 };
 bool ln_linear_supported(const LnLinearParams& params);
+// Whether the fused kernel is the faster choice over LayerNorm + projection as two
+// launches: it is when at most two workgroups share a 64-row block (each of them
+// normalises the block's rows again): 8192 rows of width 640 on 256 CUs, not 2048
+// rows of width 1280 (measured 27.1 / 42.1 us against 4.1 + 15.9 / 3.8 + 23.6 us).
+bool ln_linear_preferred(const LnLinearParams& params, int compute_units);
 hipError_t launch_ln_linear(const LnLinearParams& params, int compute_units, hipStream_t stream);
 
 struct QuantizeParams {

@@ -220,7 +220,7 @@ def test_cross_sublayer_workspace_and_validation():
 
 
 @pytest.mark.parametrize("kw,status", [
-    (dict(k=1280), sh.UNSUPPORTED),          # only width 640 is fused
+    (dict(k=960), sh.UNSUPPORTED),           # only widths 640 and 1280 are fused
     (dict(n=192), sh.UNSUPPORTED),           # n % 128 != 0
     (dict(w_dtype=sh.F16), sh.UNSUPPORTED),  # E4M3 weights only
     (dict(residual_row_stride=640), sh.INVALID_ARGUMENT),

@@ -187,21 +187,27 @@ def test_linear_strided_in_place_residual():
 
 # ---------------------------------------------------------------- LayerNorm fused into the projection
 
-@pytest.mark.parametrize("M,N,bias,strided", [(8192, 1920, False, False), (8100, 1920, True, False),
-                                              (200, 640, True, True), (1, 128, False, False),
-                                              (4096, 128, False, True), (130, 3840, True, False),
-                                              (1000, 1920, False, False), (15360, 1920, True, False)])
-def test_layer_norm_linear(M, N, bias, strided):
-    """sdxl_layer_norm_linear (norm1 -> q|k|v at width 640) equals sdxl_layer_norm followed by
+@pytest.mark.parametrize("M,N,bias,strided,K", [(8192, 1920, False, False, 640), (8100, 1920, True, False, 640),
+                                                (200, 640, True, True, 640), (1, 128, False, False, 640),
+                                                (4096, 128, False, True, 640), (130, 3840, True, False, 640),
+                                                (1000, 1920, False, False, 640), (15360, 1920, True, False, 640),
+                                                (2048, 3840, False, False, 1280), (2000, 3840, True, False, 1280),
+                                                (2048, 1280, True, True, 1280), (70, 1280, False, False, 1280),
+                                                (1, 128, True, False, 1280), (3840, 3840, False, False, 1280),
+                                                (300, 2560, True, True, 1280)])
+def test_layer_norm_linear(M, N, bias, strided, K):
+    """sdxl_layer_norm_linear (norm1 -> q|k|v at width 640 and 1280; at 1280 the kernel keeps K
+    columns 640-1279 of the normalised rows in LDS) equals sdxl_layer_norm followed by
     sdxl_linear bit for bit (same LayerNorm rounding, same fp32 sums), and the oracle's fp32
     LayerNorm, rounded to fp16 as the reference stores it, then linear on the dequantised
     weights, within the linear bar. Non-trivial gamma/beta; ragged row blocks (8100, 200, 130,
     1); one- and several-chunk column ranges, uneven splits (1000 rows: 15 chunks over 16
     workgroups of a row block is capped at one chunk each; 130 x 3840: 30 chunks, two
     workgroups of at most 2048 columns; 15360 rows, configs[4]'s level 1: 240 row blocks, every
-    workgroup on all 15 chunks); strided x and c."""
-    K = 640
-    print(f"ln_linear M{M} N{N} bias{bias} strided{strided}", flush=True)
+    workgroup on all 15 chunks; width 1280: the level-2 q|k|v [2048, 3840] and q [2048, 1280],
+    configs[4]'s level 2 [3840, 3840], at most 1024 columns per workgroup: 300 x 2560 splits 20
+    chunks in two); strided x and c."""
+    print(f"ln_linear M{M} N{N} K{K} bias{bias} strided{strided}", flush=True)
     xb = oracle.normal_f16(1100 + M, (M, K))
     gb = oracle.normal_f16(1101, (K,), 0.5)
     bb = oracle.normal_f16(1102, (K,), 0.5)
@@ -235,15 +241,16 @@ def test_layer_norm_linear(M, N, bias, strided):
     assert (err <= bound).all(), float(err.max())
 
 
-@pytest.mark.parametrize("M,N,bias", [(8192, 1920, False), (8100, 1920, True), (130, 3840, True), (1, 128, False),
-                                      (1000, 1920, False), (15360, 1920, False)])
-def test_layer_norm_linear_e4m3_activations(M, N, bias):
+@pytest.mark.parametrize("M,N,bias,K", [(8192, 1920, False, 640), (8100, 1920, True, 640), (130, 3840, True, 640),
+                                        (1, 128, False, 640), (1000, 1920, False, 640), (15360, 1920, False, 640),
+                                        (2048, 3840, False, 1280), (2000, 1280, True, 1280), (70, 3840, True, 1280),
+                                        (3840, 3840, False, 1280)])
+def test_layer_norm_linear_e4m3_activations(M, N, bias, K):
     """sdxl_layer_norm_linear_e4m3 (E4M3 LayerNorm rows with per-row scales, fp8 MFMA, inside one
     kernel) equals sdxl_layer_norm_e4m3 followed by sdxl_linear_e4m3 bit for bit; the product
     part against the fp64 product of the decoded codes (the E4M3 LayerNorm itself is pinned to
-    the oracle by test_layer_norm_e4m3)."""
-    K = 640
-    print(f"ln_linear e4m3 M{M} N{N} bias{bias}", flush=True)
+    the oracle by test_layer_norm_e4m3); widths 640 and 1280."""
+    print(f"ln_linear e4m3 M{M} N{N} K{K} bias{bias}", flush=True)
     xb = oracle.normal_f16(1120 + M, (M, K))
     gb = oracle.normal_f16(1121, (K,), 0.5)
     bb = oracle.normal_f16(1122, (K,), 0.5)
@@ -265,15 +272,19 @@ def test_layer_norm_linear_e4m3_activations(M, N, bias):
     within_half_ulp(host(got)[rows], ref, 1e-4, f"LN E4M3 + linear {M}x{N}")
 
 
-def test_sublayer_layer_norm_fusion_switch():
-    """configs[3] sublayer with the LayerNorm inside the q|k|v projection (default) and as its own
-    launch (ln_fusion off), fp16 and E4M3 activations: the same bits."""
-    x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(2, 4096, 10, 1110)
-    gamma = dev16(oracle.normal_f16(1111, (640,), 0.5))
-    beta = dev16(oracle.normal_f16(1112, (640,), 0.5))
+@pytest.mark.parametrize("B,S,H", [(2, 4096, 10), (2, 1024, 20)])
+def test_sublayer_layer_norm_fusion_switch(B, S, H):
+    """configs[3] sublayer and the level-2 self half ([2, 1024, 1280], 20 heads) with the default
+    LayerNorm placement (inside the q|k|v projection at level 1; its own launch at level 2, where
+    that is faster) and with the LayerNorm as its own launch (ln_fusion off), fp16 and E4M3
+    activations: the same bits."""
+    W = 64 * H
+    x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(B, S, H, 1110)
+    gamma = dev16(oracle.normal_f16(1111, (W,), 0.5))
+    beta = dev16(oracle.normal_f16(1112, (W,), 0.5))
     for fp8 in (False, True):
-        y1 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, fp8_activations=fp8)
-        y2 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, 10, fp8_activations=fp8, ln_fusion=False)
+        y1 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, fp8_activations=fp8)
+        y2 = sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, fp8_activations=fp8, ln_fusion=False)
         torch.cuda.synchronize()
         assert torch.equal(y1, y2), fp8
 
@@ -596,14 +607,14 @@ def test_random_projection_and_layer_norm_shapes(seed):
             ref = torch.nn.functional.layer_norm(x.float(), (W,), gm.float(), bt.float(), 1e-5)
             bound = 2.0 ** -10 * ref.abs() + 2e-3 * gm.float().abs() + 1e-4
         else:
-            K, N = 640, 128 * rng.randint(1, 16)
+            K, N = rng.choice([640, 1280]), 128 * rng.randint(1, 16)
             x = torch.randn(M, K, device="cuda", generator=g).half()
             gm = (1 + 0.1 * torch.randn(K, device="cuda", generator=g)).half()
             bt = (0.1 * torch.randn(K, device="cuda", generator=g)).half()
             wq, ws = sh.quantize_e4m3_rows((torch.randn(N, K, device="cuda", generator=g) * 0.05).half())
             bias = torch.randn(N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
             fp8 = kind == "lnlin8"
-            label = f"{kind} M{M} N{N} bias={bias is not None}"
+            label = f"{kind} M{M} N{N} K{K} bias={bias is not None}"
             print(label, flush=True)
             got = sh.layer_norm_linear(x, gm, bt, wq, ws, bias=bias, fp8_activations=fp8)
             if fp8:
