@@ -130,10 +130,15 @@ __device__ __forceinline__ f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
 // each wave's 32 x 64 block is one 32-row query block of one head) fused
 // with the attention over kKvG 32-key groups of context (kKvHalf: the last
 // group holds at most 16 keys); see the epilogue.
+// kProd: the workgroup has kWM x kWN more waves that only issue the stage
+// transfers (wave w + kWM kWN issues compute wave w's), so the compute waves
+// never stall on a transfer's issue and the producers' issue overlaps the
+// MFMA work of their SIMD.
 template <bool kWFp8, bool kAFp8, int kTM, int kRing, int kOcc, bool kNt, int kWM = 2, int kKvG = 0, bool kKvHalf = false,
-          int kWN = 2>
-__global__ __launch_bounds__(64 * kWM * kWN, kOcc) void linear_kernel(LinearParams p) {
+          int kWN = 2, bool kProd = false>
+__global__ __launch_bounds__(64 * kWM * kWN * (kProd ? 2 : 1), kOcc) void linear_kernel(LinearParams p) {
     static_assert(!kAFp8 || kWFp8, "E4M3 activations need E4M3 weights");
+    static_assert(!kProd || kKvG == 0, "producer waves: plain projections only");
     static_assert(kKvG == 0 || kWN == 2, "the cross-attention form uses 128-column tiles");
     constexpr int kBMt = 64 * kTM;
     constexpr int kBNt = 64 * kWN;             // tile columns
@@ -161,7 +166,9 @@ __global__ __launch_bounds__(64 * kWM * kWN, kOcc) void linear_kernel(LinearPara
     __shared__ __attribute__((aligned(16))) char vbuf[2 * kVRows * kRowBytes];
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool producer = kProd && wave_id >= kWaves;
+    const int wave = kProd ? wave_id % kWaves : wave_id;  // compute wave (or the one a producer serves)
     const int hf = lane >> 5, col = lane & 31;
 
     // Tasks in groups of group_m m blocks (within a group m varies fastest,
@@ -294,11 +301,8 @@ __global__ __launch_bounds__(64 * kWM * kWN, kOcc) void linear_kernel(LinearPara
             lds_dma16(vb0 + hl * 128, off, lds_addr(vbuf + (hl * kVRows + 8 * r8) * kRowBytes));
         }
     }
-#pragma unroll
-    for (int st = 0; st < kRing - 1; ++st)
-        if (st < n_stages) issue_stage(st);
-    for (int s = 0; s < n_stages; ++s) {
-        // Stage s landed (this wave's transfers; later stages may still fly) ...
+    auto wait_stage = [&](int s) __attribute__((always_inline)) {
+        // Stage s landed (this wave's transfers; later stages may still fly)
         const int later = min(n_stages - 1 - s, kRing - 2);
         if constexpr (kRing >= 4) {
             if (later >= 2) wait_vmem<2 * kLoadsPerStage>();
@@ -310,8 +314,32 @@ __global__ __launch_bounds__(64 * kWM * kWN, kOcc) void linear_kernel(LinearPara
         } else {
             wait_vmem<0>();
         }
-        __syncthreads();  // ... for every wave, and stage s - 1's buffers are free
-        if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
+    };
+    if constexpr (kProd) {
+        if (producer) {
+            // the compute waves' barrier sequence: one per stage, one before the epilogue
+#pragma unroll
+            for (int st = 0; st < kRing - 1; ++st)
+                if (st < n_stages) issue_stage(st);
+            for (int s = 0; s < n_stages; ++s) {
+                wait_stage(s);
+                __syncthreads();
+                if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
+            }
+            __syncthreads();
+            return;
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < kRing - 1; ++st)
+            if (st < n_stages) issue_stage(st);
+    }
+    for (int s = 0; s < n_stages; ++s) {
+        if constexpr (!kProd) wait_stage(s);
+        __syncthreads();  // stage s landed for every wave, and stage s - 1's buffers are free
+        if constexpr (!kProd) {
+            if (s + kRing - 1 < n_stages) issue_stage(s + kRing - 1);
+        }
         const char* ab = smem[s % kRing];
         const char* wb = smem[s % kRing] + kATileBytes;
         if constexpr (kAFp8) {
@@ -1472,6 +1500,13 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
         if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, true>), grid, block, 0, stream, p);      \
         else hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, 2, false>), grid, block, 0, stream, p);        \
     } while (0)
+    // ... with four producer waves (512 threads)
+#define SDXL_LIN_PROD(WF, AF, TM, RING, OCC)                                                                    \
+    do {                                                                                                        \
+        const dim3 bp(512);                                                                                     \
+        if (nt) hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, OCC, true, 2, 0, false, 2, true>), grid, bp, 0, stream, p); \
+        else hipLaunchKernelGGL((linear_kernel<WF, AF, TM, RING, OCC, false, 2, 0, false, 2, true>), grid, bp, 0, stream, p); \
+    } while (0)
     // E4M3 weights: 256 x 128 tiles of 8 waves (4 x 2, each 64 x 64; two
     // workgroups per CU) when those tiles give at least 90 % of the CUs one:
     // each staged W tile serves twice the rows, four waves share each SIMD.
@@ -1513,18 +1548,37 @@ hipError_t launch_linear(const LinearParams& params_in, bool w_fp8, int compute_
         }
         return hipGetLastError();
     }
+    // 64-row tiles of few workgroups per CU (the level-2 projections, the
+    // per-request context K/V projection) wait on their stage transfers
+    // (rocprof: 59 % of wave time in s_waitcnt, 11 % MFMA-busy on the
+    // level-2 out-projection): there producer waves issue the transfers and,
+    // with fp16 weights, a deeper ring requests each stage further ahead.
+    // Measured (graph replay, fp16 weights): one round of tiles, ring of four
+    // (96 KiB: one workgroup per CU) + producers: context K/V [154, 2048] x
+    // [2048, 2560] 20.8 -> 12.0 us, x [2048, 1280] 15.3 -> 11.1 us; at most
+    // 1.25 tiles per CU, ring of three + producers: 2048 x 1280 x 1280 + bias +
+    // residual 16.5 -> 15.0 us; E4M3 weights, producers on the two-stage
+    // ring: 13.1 -> 12.6 us (2048 x 1280 x 1280), context K/V 15.6 -> 12.0 us.
+    // With more tiles per CU (8192 x 640 x 640, 3840 x 1280 x 1280) both
+    // measured slower than the plain four-wave kernel.
+    const int cus_lin = compute_units > 0 ? compute_units : 256;
+    const bool one_round = tasks <= cus_lin, few = tasks * 4 <= (int64_t)cus_lin * 5;
     if (a_fp8) {
         if (use_tall) SDXL_LIN(true, true, 4, 3);
         else if (use_short) SDXL_LIN(true, true, 1, 2);
         else SDXL_LIN(true, true, 2, 3);
     } else if (w_fp8) {
         if (use_tall) SDXL_LIN(true, false, 4, 2);
+        else if (use_short && few) SDXL_LIN_PROD(true, false, 1, 2, 2);
         else if (use_short) SDXL_LIN(true, false, 1, 2);
         else SDXL_LIN(true, false, 2, 3);
     } else {
-        if (use_short) SDXL_LIN(false, false, 1, 2);
+        if (use_short && one_round) SDXL_LIN_PROD(false, false, 1, 4, 1);
+        else if (use_short && few) SDXL_LIN_PROD(false, false, 1, 3, 2);
+        else if (use_short) SDXL_LIN(false, false, 1, 2);
         else SDXL_LIN(false, false, 2, 2);
     }
+#undef SDXL_LIN_PROD
 #undef SDXL_LIN
     return hipGetLastError();
 }
