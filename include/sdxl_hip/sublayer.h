@@ -155,7 +155,9 @@ sdxl_status sdxl_attn_sublayer(const sdxl_sublayer_desc* desc, const void* x, co
  * 75 MiB). Every call on one GPU shares that array: calls that overlap on one GPU
  * (concurrent streams, or threads without ordering) race. Allocates nothing, no
  * host synchronisation; the first call on a device looks up the array's address.
- * Arguments and results as sdxl_attn_sublayer. */
+ * The array is part of the library's code object: a process that loads the library
+ * reserves its 80 MiB on every GPU it runs one of the library's kernels on, whether
+ * or not it calls this entry point. Arguments and results as sdxl_attn_sublayer. */
 size_t sdxl_attn_sublayer_noalloc_max_workspace_bytes(void);
 sdxl_status sdxl_attn_sublayer_noalloc(const sdxl_sublayer_desc* desc, const void* x, const void* ln_gamma,
                                        const void* ln_beta, const void* w_qkv, const float* w_qkv_scale,
