@@ -171,6 +171,36 @@ def test_linear_e4m3_qkv(M, N):
     within_half_ulp(got[rows], ref, 1e-4, f"linear E4M3 {M}x{N}x{K}")
 
 
+# Shapes of the producer-wave forms on a 256-CU device (64-row tiles, few workgroups per CU):
+# fp16 weights with one round of tiles (ring of four: the per-request context K/V projections, a
+# ragged 70-row call), at most 1.25 tiles per CU (ring of three: the level-2 out-projection, a
+# ragged last row and column tile), and E4M3 weights (ring of two); in place over the residual.
+@pytest.mark.parametrize("M,N,K,w8", [(154, 2560, 2048, False), (154, 1280, 2048, False), (70, 1000, 1280, False),
+                                      (2048, 1280, 1280, False), (2040, 1276, 1280, False),
+                                      (2048, 1280, 1280, True), (1990, 1220, 1280, True), (154, 2560, 2048, True)])
+def test_linear_producer_waves(M, N, K, w8):
+    """The projection forms whose transfers are issued by producer waves (deeper rings with fp16
+    weights) against the fp32 oracle within half an fp16 ulp, with bias and residual, and in
+    place (c over the residual: each element's residual read by the lane that writes it)."""
+    print(f"linear producers M{M} N{N} K{K} w8={w8}", flush=True)
+    ab = oracle.normal_f16(960 + M, (M, K))
+    bb = oracle.normal_f16(962, (N,), 0.02)
+    rb = oracle.normal_f16(963, (M, N))
+    if w8:
+        q, sc = oracle.quantize_e4m3_rows(oracle.normal_f32(961 + N, (N, K), 0.02))
+        w, ws, w32 = torch.from_numpy(q).to(DEV), torch.from_numpy(sc).to(DEV), oracle.dequantize_e4m3_rows(q, sc)
+    else:
+        wb = oracle.normal_f16(961 + N, (N, K), 0.02)
+        w, ws, w32 = dev16(wb), None, oracle.f16_bits_to_f32(wb)
+    got = host(sh.linear(dev16(ab), w, w_scale=ws, bias=dev16(bb), residual=dev16(rb)))
+    ref = _linear_ref(ab, w32, bb, rb)
+    within_half_ulp(got, ref, 1e-4, f"linear producers {M}x{N}x{K} w8={w8}")
+    y = dev16(rb)
+    sh.linear(dev16(ab), w, w_scale=ws, bias=dev16(bb), residual=y, out=y)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y), got)
+
+
 def test_linear_strided_in_place_residual():
     """a as a column slice of a wider buffer, c written over the residual (y += x W^T + b)."""
     M, K, N = 200, 640, 640
