@@ -34,6 +34,13 @@ struct LinearParams {
 };
 // compute_units: CUs of the device (tile-size choice).
 hipError_t launch_linear(const LinearParams& params, bool w_fp8, int compute_units, hipStream_t stream);
+// K-split form for fp16 weights (64 x 160 tiles, the four waves of a tile each
+// over a quarter of every K stage): used by launch_linear when it applies.
+// Requires a residual (output projections), n % 8 == 0, 16-byte aligned rows
+// and pointers (a, w, c, residual, bias, w_scale) and one round of tiles on
+// compute_units CUs.
+bool linear_ksplit_supported(const LinearParams& params, bool w_fp8, int compute_units);
+hipError_t launch_linear_ksplit(const LinearParams& params, hipStream_t stream);
 // q = a w^T (64 x 128 tiles, one 32-row block of one head per wave), then
 // softmax(q k^T * scale) v per head, written to c. Requires seq % 64 == 0,
 // n % 128 == 0 (heads of 64), 65 <= ctx_len <= 80, k % 64 == 0, no bias or

@@ -201,6 +201,30 @@ def test_linear_producer_waves(M, N, K, w8):
     assert np.array_equal(host(y), got)
 
 
+# Shapes of the K-split form (output projections: a residual; 64 x 160 tiles, one round on a
+# 256-CU device: n % 8 == 0 and 230-256 tiles): the level-2 out-projection, ragged last row and
+# column tiles, no bias; without a residual the same shapes run the 64 x 128 kernel.
+@pytest.mark.parametrize("M,N,K,bias", [(2048, 1280, 1280, True), (1990, 1272, 1280, True), (2048, 1280, 640, False),
+                                        (1900, 1280, 2048, True)])
+def test_linear_k_split(M, N, K, bias):
+    """The K-split projection (four waves per tile, each over a quarter of every K stage, partial
+    tiles summed through LDS in a fixed order) against the fp32 oracle within half an fp16 ulp, and
+    in place over the residual, bit-equal to the out-of-place call."""
+    print(f"linear k-split M{M} N{N} K{K} bias={bias}", flush=True)
+    ab = oracle.normal_f16(970 + M, (M, K))
+    wb = oracle.normal_f16(971 + N, (N, K), 0.02)
+    bb = oracle.normal_f16(972, (N,), 0.02) if bias else None
+    rb = oracle.normal_f16(973, (M, N))
+    w32 = oracle.f16_bits_to_f32(wb)
+    b_dev = dev16(bb) if bias else None
+    got = host(sh.linear(dev16(ab), dev16(wb), bias=b_dev, residual=dev16(rb)))
+    within_half_ulp(got, _linear_ref(ab, w32, bb, rb), 1e-4, f"linear k-split {M}x{N}x{K}")
+    y = dev16(rb)
+    sh.linear(dev16(ab), dev16(wb), bias=b_dev, residual=y, out=y)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(y), got)
+
+
 def test_linear_strided_in_place_residual():
     """a as a column slice of a wider buffer, c written over the residual (y += x W^T + b)."""
     M, K, N = 200, 640, 640
