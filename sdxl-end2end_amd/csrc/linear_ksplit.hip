@@ -148,21 +148,24 @@ __global__ __launch_bounds__(256, 1) void linear_ksplit_kernel(LinearParams p) {
     };
 
     // epilogue operands, requested first so that their latency hides under
-    // the loop. Wave w finishes rows 8w .. 8w + 7 of every 32-row m-tile: item
-    // q = lane + 64 it (it < kIt) is row r = q / kDC of those (m-tile r / 8,
-    // row 8w + r % 8) and the 8 columns 8 dc .. 8 dc + 7, dc = q % kDC, so that
-    // residual loads and output stores are 16 bytes per lane and every row's
-    // columns are contiguous across lanes.
+    // the loop. Wave w finishes rows 8w .. 8w + 7 of both 32-row m-tiles:
+    // lane l takes row r = 4 (l / 16) + (l / 4) % 4 of those 16 (m-tile r / 8,
+    // row 8w + r % 8) and, in item it (it < kIt), the 8 columns 8 dc .. 8 dc +
+    // 7 with dc = 4 it + l % 4: residual loads and output stores are 16 bytes
+    // per lane, 64 contiguous bytes per row, and the partial reads of every 16
+    // lanes (4 rows x 4 column groups) hit 16 distinct bank groups.
+    static_assert(kMT == 2, "16 rows per wave in the epilogue");
     constexpr int kDC = 4 * kNT;                 // 8-column groups per row
-    constexpr int kIt = 8 * kMT * kDC / 64;
-    static_assert(kIt * 64 == 8 * kMT * kDC, "epilogue items per lane");
+    constexpr int kIt = kDC / 4;
+    const int er = 4 * (lane >> 4) + ((lane >> 2) & 3);
+    const int ei = er >> 3, erow = 8 * wave + (er & 7);
     f32x4 e_scale[kIt][2];
     f16x8 e_bias[kIt], res[kIt];
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-        const int q = lane + 64 * it, r = q / kDC, dc = q % kDC;
+        const int dc = 4 * it + (lane & 3);
         const int en = min(n0 + 8 * dc, p.n - 8);
-        const int m = min(m0 + 32 * (r >> 3) + 8 * wave + (r & 7), p.m - 1);
+        const int m = min(m0 + 32 * ei + erow, p.m - 1);
         if (p.w_scale != nullptr) {
             e_scale[it][0] = *(const f32x4*)(p.w_scale + en);
             e_scale[it][1] = *(const f32x4*)(p.w_scale + en + 4);
@@ -216,17 +219,18 @@ __global__ __launch_bounds__(256, 1) void linear_ksplit_kernel(LinearParams p) {
     }
 
     // ---- the four partial tiles through LDS (all of them at once: 4 x 40 KiB
-    // per 32-row m-tile, the whole 160 KiB). Wave w parks its partial row-major (chunk c of row r
-    // at c ^ ((r >> 1) & 7): conflict-free for 16 lanes of distinct rows and
-    // for the readers' two rows of 8 chunks); acc[j][i][4u + q] is row 32i +
-    // col, column 32j + 8u + 4hf + q of the tile.
+    // per 32-row m-tile, the whole 160 KiB). Wave w parks its partial
+    // row-major, 16-byte chunk c of row r of m-tile i at c ^ sw(i, r) with
+    // sw = ((r >> 1) & 7) ^ 4i: conflict-free for the 16 rows of a parking
+    // write and for the readers' 4 rows (two m-tiles) x 4 chunk pairs;
+    // acc[j][i][4u + q] is row 32i + col, column 32j + 8u + 4hf + q of the tile.
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();  // every wave is done with the stage buffers
     {
-        const int psw = (col >> 1) & 7;
 #pragma unroll
         for (int i = 0; i < kMT; ++i) {
             char* mine = smem_raw + (i * 4 + wave) * kPartBytes;
+            const int psw = ((col >> 1) & 7) ^ (4 * i);
 #pragma unroll
             for (int j = 0; j < kNT; ++j)
 #pragma unroll
@@ -241,11 +245,10 @@ __global__ __launch_bounds__(256, 1) void linear_ksplit_kernel(LinearParams p) {
     __builtin_amdgcn_s_barrier();
 #pragma unroll
     for (int it = 0; it < kIt; ++it) {
-        const int q = lane + 64 * it, r = q / kDC, dc = q % kDC;
-        const int i = r >> 3, row = 8 * wave + (r & 7);
-        const int m = m0 + 32 * i + row, en = n0 + 8 * dc;
-        const char* part = smem_raw + i * 4 * kPartBytes + row * kPartRow;
-        const int sw = (row >> 1) & 7;
+        const int dc = 4 * it + (lane & 3);
+        const int m = m0 + 32 * ei + erow, en = n0 + 8 * dc;
+        const char* part = smem_raw + ei * 4 * kPartBytes + erow * kPartRow;
+        const int sw = ((erow >> 1) & 7) ^ (4 * ei);
         f32x4 a[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
