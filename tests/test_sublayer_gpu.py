@@ -626,15 +626,18 @@ def test_random_projection_and_layer_norm_shapes(seed):
     import random
     rng = random.Random(2000 + seed)
     for n in range(40):
-        kind = rng.choice(["lin16", "lin8", "ln", "lnlin", "lnlin8"])
+        kind = rng.choice(["lin16", "lin16ks", "lin8", "ln", "lnlin", "lnlin8"])
         M = rng.choice([rng.randint(1, 300), rng.randint(1, 5000)])
         g = torch.Generator(device="cuda").manual_seed(seed * 1000 + n)
-        if kind in ("lin16", "lin8"):
+        if kind in ("lin16", "lin16ks", "lin8"):
             K, N = 64 * rng.randint(1, 24), 4 * rng.randint(1, 768)
+            if kind == "lin16ks":  # shapes of the K-split form on 256 CUs: 232-256 tiles of 64 x 160, a residual
+                M, N = rng.randint(1793, 2048), 8 * rng.randint(141, 160)
             a = torch.randn(M, K, device="cuda", generator=g).half()
             w = (torch.randn(N, K, device="cuda", generator=g) * 0.05).half()
             bias = torch.randn(N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
-            res = torch.randn(M, N, device="cuda", generator=g).half() if rng.random() < 0.5 else None
+            res = (torch.randn(M, N, device="cuda", generator=g).half()
+                   if kind == "lin16ks" or rng.random() < 0.5 else None)
             label = f"{kind} M{M} N{N} K{K} bias={bias is not None} residual={res is not None}"
             print(label, flush=True)
             if kind == "lin8":
