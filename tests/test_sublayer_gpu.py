@@ -225,6 +225,30 @@ def test_linear_k_split(M, N, K, bias):
     assert np.array_equal(host(y), got)
 
 
+def test_linear_k_split_strided():
+    """The K-split form on strided operands: a a column slice of a wider buffer, w rows padded, the
+    residual and the output column slices of wider buffers (in place and out of place)."""
+    M, N, K = 2048, 1280, 1280
+    ab = oracle.normal_f16(980, (M, 3 * K))
+    wb = oracle.normal_f16(981, (N, K + 64), 0.02)
+    bb = oracle.normal_f16(982, (N,), 0.02)
+    rb = oracle.normal_f16(983, (M, 2 * N))
+    a = dev16(ab)[:, K:2 * K]
+    w = dev16(wb)[:, :K]
+    ref = _linear_ref(np.ascontiguousarray(ab[:, K:2 * K]), oracle.f16_bits_to_f32(np.ascontiguousarray(wb[:, :K])),
+                      bb, np.ascontiguousarray(rb[:, N:]))
+    outbuf = torch.zeros(M, 2 * N, dtype=torch.float16, device=DEV)
+    resbuf = dev16(rb)
+    sh.linear(a, w, bias=dev16(bb), residual=resbuf[:, N:], out=outbuf[:, :N])
+    got = host(outbuf[:, :N])
+    within_half_ulp(got, ref, 1e-4, "linear k-split strided")
+    assert not host(outbuf[:, N:]).any()  # nothing written past the output columns
+    sh.linear(a, w, bias=dev16(bb), residual=resbuf[:, N:], out=resbuf[:, N:])
+    torch.cuda.synchronize()
+    assert np.array_equal(host(resbuf[:, N:]), got)
+    assert np.array_equal(host(resbuf[:, :N]), oracle.f16_bits_to_f32(rb[:, :N]))
+
+
 def test_linear_strided_in_place_residual():
     """a as a column slice of a wider buffer, c written over the residual (y += x W^T + b)."""
     M, K, N = 200, 640, 640
