@@ -225,6 +225,36 @@ void sublayer_cases() {
     std::cout << "sublayer cases passed\n";
 }
 
+// The level-2 out-projection shape ([2, 1024, 1280] x [1280, 1280]^T + bias, added into the hidden
+// state: the K-split kernel on a 256-CU device): sampled rows against the host fp32 reference of the
+// fp16-rounded operands.
+void out_projection_cases() {
+    Runtime runtime;
+    Ops ops(runtime);
+    const std::size_t rows = 2048, W = 1280;
+    const auto a = filled({2, rows / 2, W}, [](std::size_t i) { return std::sin(static_cast<float>(i % 9973) * 0.37F); });
+    const auto w = filled({W, W}, [](std::size_t i) { return std::cos(static_cast<float>(i % 7919) * 0.11F) * 0.03F; });
+    const auto b = filled({W}, [](std::size_t i) { return std::sin(static_cast<float>(i) * 0.7F) * 0.1F; });
+    const auto h = filled({2, rows / 2, W}, [](std::size_t i) { return std::cos(static_cast<float>(i % 6007) * 0.05F); });
+    const auto ad = Tensor::from_host_f32(runtime, a);
+    const auto wd = Tensor::from_host_f32(runtime, w);
+    const auto bd = Tensor::from_host_f32(runtime, b);
+    auto hd = Tensor::from_host_f32(runtime, h);
+    const auto a16 = ad.to_host_f32(runtime).values, w16 = wd.to_host_f32(runtime).values;
+    const auto b16 = bd.to_host_f32(runtime).values, h16 = hd.to_host_f32(runtime).values;
+    ops.linear_residual_into(ad, wd, &bd, hd);
+    const auto got = hd.to_host_f32(runtime).values;
+    for (std::size_t r : {std::size_t{0}, std::size_t{1}, std::size_t{63}, std::size_t{64}, std::size_t{1023},
+                          std::size_t{1500}, rows - 1}) {
+        const auto ref = host_linear(std::vector<float>(a16.begin() + r * W, a16.begin() + (r + 1) * W), w16, 1, W, W);
+        for (std::size_t o = 0; o < W; ++o) {
+            const float e = ref[o] + b16[o] + h16[r * W + o];
+            require_close(got[r * W + o], e, std::fabs(e) * 1e-3F + 1e-3F, "out-projection");
+        }
+    }
+    std::cout << "out-projection cases passed\n";
+}
+
 // Ops::attention itself (allocating its output) captured in a HIP graph: after
 // one warm-up call the arena serves the output from its cache, so the capture
 // makes no driver allocation; replays with eager work between them reproduce
@@ -426,6 +456,7 @@ void device_cases() {
     graph_capture_cases();
     std::cout << "device cases passed\n";
     sublayer_cases();
+    out_projection_cases();
 }
 
 }  // namespace

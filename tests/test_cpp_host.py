@@ -32,6 +32,7 @@ def test_device_cases():
     assert r.returncode == 0, r.stdout + r.stderr
     assert "device cases passed" in r.stdout
     assert "sublayer cases passed" in r.stdout
+    assert "out-projection cases passed" in r.stdout  # the level-2 out-projection shape (K-split kernel)
     assert "graph capture cases passed" in r.stdout  # Ops::attention captured in a HIP graph
 
 
