@@ -768,3 +768,40 @@ def test_random_sublayers_equal_their_compositions(seed):
         torch.cuda.synchronize()
         assert torch.equal(y, y2), label
         done += 1
+
+
+def test_level2_sublayers_hip_graph_replays():
+    """The level-2 self and cross sublayer calls (LayerNorm, projections incl. the K-split
+    out-projection, attention) captured in one HIP graph: no allocation or memset inside the
+    calls; four replays with unrelated eager work between them each equal the eager results."""
+    B, S, H = 2, 1024, 20
+    x, gamma, beta, q8, s8, w_out, b_out = _sublayer_inputs(B, S, H, 1500)
+    cx, cg, cb, ctx, w_kv, w_q, w_q_scale, cw_out, cb_out = _cross_inputs(B, S, H, 1600)
+    kv = sh.project_context_kv(ctx, w_kv)
+    y_self, y_cross = torch.empty_like(x), torch.empty_like(cx)
+    ws_self = torch.empty(1 << 26, dtype=torch.uint8, device=DEV)
+    ws_cross = torch.empty(1 << 26, dtype=torch.uint8, device=DEV)
+
+    def calls():
+        sh.attn_sublayer(x, gamma, beta, q8, s8, w_out, b_out, H, out=y_self, workspace=ws_self)
+        sh.cross_attn_sublayer(cx, cg, cb, w_q, w_q_scale, kv, cw_out, cb_out, H, out=y_cross, workspace=ws_cross)
+
+    calls()
+    torch.cuda.synchronize()
+    eager_self, eager_cross = y_self.clone(), y_cross.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        calls()  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        calls()
+    for i in range(4):
+        y_self.fill_(float("nan"))
+        y_cross.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_self, eager_self), i
+        assert torch.equal(y_cross, eager_cross), i
+        _ = (x.float() * 2).sum().item()  # unrelated eager work between replays
