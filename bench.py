@@ -47,7 +47,7 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="skip the other configs")
-    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,vae,clip,torch_sdpa,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8,l2_outproj,l1_outproj,l2_qkv,l2_ln) and exit")
+    ap.add_argument("--only", default="", help="profiling aid: run only this config (c1,c2,c3,c4,c5...,l2self,cross,l1cross,vae,clip,torch_sdpa,qkv,qkv_fp8,ln_qkv,ln_qkv_fp8,l2_outproj,l1_outproj,l2_qkv,l2_ln) and exit")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="profiling aid: run device-to-device copies of MIB MiB (HBM counter calibration) and exit")
     return ap.parse_args()
@@ -315,11 +315,12 @@ def bench_vae_attention(torch, sh, steps=5, warmup=2):
     return out
 
 
-def bench_cross_sublayer(torch, sh, steps=50, warmup=5):
-    """The cross-attention half of a level-2 transformer block (32x32 latent, 20 heads): hidden
-    [2, 1024, 1280] -> LayerNorm -> to_q -> attention against the 77-token context's K|V (projected
-    once per request from [2, 77, 2048], timed separately) -> to_out + bias + residual."""
-    B, S, H, L, C = 2, 1024, 20, 77, 2048
+def bench_cross_sublayer(torch, sh, steps=50, warmup=5, S=1024, H=20):
+    """The cross-attention half of a transformer block (defaults: level 2, 32x32 latent, 20 heads;
+    S=4096, H=10: level 1): hidden [2, S, 64 H] -> LayerNorm -> to_q -> attention against the
+    77-token context's K|V (projected once per request from [2, 77, 2048], timed separately) ->
+    to_out + bias + residual."""
+    B, L, C = 2, 77, 2048
     W, M = H * 64, B * S
     g = torch.Generator(device="cuda:0")
     g.manual_seed(11)
@@ -488,6 +489,9 @@ def main():
     if args.only == "cross":
         print(json.dumps(bench_cross_sublayer(torch, sh, args.steps, args.warmup)), flush=True)
         return
+    if args.only == "l1cross":
+        print(json.dumps(bench_cross_sublayer(torch, sh, args.steps, args.warmup, S=4096, H=10)), flush=True)
+        return
     if args.only == "vae":
         print(json.dumps(bench_vae_attention(torch, sh, args.steps, args.warmup)), flush=True)
         return
@@ -624,6 +628,14 @@ def main():
         sec["c4_sublayer"] = bench_sublayer(torch, sh)
         sec["l2_self_sublayer"] = bench_sublayer(torch, sh, B=2, S=1024, H=20)
         sec["l2_cross_sublayer"] = bench_cross_sublayer(torch, sh)
+        sec["l1_cross_sublayer"] = bench_cross_sublayer(torch, sh, S=4096, H=10)
+        # SDXL's UNet holds 70 transformer blocks: 60 at level 2 ([2, 1024, 1280]), 10 at level 1
+        # ([2, 4096, 640]); each runs a self- and a cross-attention sublayer. Sum of this run's
+        # fused sublayer calls over them (the per-request context K/V projections excluded): the
+        # attention path's device time per denoising step, from the measured calls above.
+        sec["unet_attention_path_per_step_us"] = round(
+            60 * (sec["l2_self_sublayer"]["fused_call_us"] + sec["l2_cross_sublayer"]["fused_call_us"])
+            + 10 * (sec["c4_sublayer"]["fused_call_us"] + sec["l1_cross_sublayer"]["fused_call_us"]), 1)
         sec["vae_mid_attention_fp32"] = bench_vae_attention(torch, sh)
         sec["torch_sdpa_comparison"] = bench_torch_sdpa(torch)
         result["secondary"] = sec
