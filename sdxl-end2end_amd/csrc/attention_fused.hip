@@ -186,6 +186,7 @@ constexpr int kKindWhole = 0;  // 4 waves: 128 query rows, all keys
 constexpr int kKindSplit = 1;  // 4 waves: 64 query rows, each row block's keys in two halves
 constexpr int kKindSplit2 = 4;  // as kKindSplit with 64 keys of each half per stage (64 KiB of LDS)
 constexpr int kKindMixed = 2;  // 12 waves: 10 consecutive 32-row blocks, 8 whole + 2 split in groups
+constexpr int kKindMixed2 = 5;  // as kKindMixed for calls whose workgroups can span two heads
 constexpr int kMixedFull = 8;    // waves of a mixed workgroup that take one row block and all keys
 constexpr int kMixedBlocks = 10; // 32-row blocks per mixed workgroup
 // Output staging after the key loop (merge slots, then 4 KiB per storing
@@ -200,7 +201,7 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                                                                      char (*ring)[kTileBytes]) {
     constexpr bool split2 = kKind == kKindSplit2;
     constexpr bool split = kKind == kKindSplit || split2;  // row assignment, merge and epilogue
-    constexpr bool mixed = kKind == kKindMixed;
+    constexpr bool mixed = kKind == kKindMixed || kKind == kKindMixed2;
     constexpr int kBlockQueries = kWaves * 32;
     constexpr int kLoadsPerWave = 16 / kWaves;  // 1-KiB transfers per wave and tile (K and V), 4-wave kinds
 
@@ -406,23 +407,60 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
                                              (int64_t)(bh_set[0] % p.heads) * kHeadDim) * elem;
     const char* set_v1 = (const char*)p.v + ((int64_t)(bh_set[1] / p.heads) * p.k_seq * p.v_row_stride +
                                              (int64_t)(bh_set[1] % p.heads) * kHeadDim) * elem;
+    // kKindMixed2 (calls whose blocks per head are not a multiple of 10, so
+    // that some workgroups stage two heads, nsets == 2, with twice the
+    // transfers): the second head's V slabs go to the half waves as well (half
+    // wave 8 + i takes V slabs p + 4r and p + 4r + 2, p = i & 1, r = i >> 1), so
+    // that the whole waves still issue one transfer per tile step (c3 86.2 ->
+    // 85.0 us). A kind of its own: the extra code in the common kind measured
+    // 0.8-1.6 % slower on calls where no workgroup spans two heads.
+    constexpr bool v1_on_half = kKind == kKindMixed2;
     const bool mixed_v = wave < kMixedFull;
     const int64_t mixed_stride = mixed_v ? vs_bytes : ks_bytes;
     const uint32_t mixed_off = mixed ? lane_off(wave & 1, mixed_stride) : 0u;
     auto issue_mixed = [&](int kt, int vt) __attribute__((always_inline)) {
         const int tile = mixed_v ? vt : kt;
-        if (tile < 0 || tile >= n_tiles) return;
+        if constexpr (!v1_on_half) {
+            if (tile < 0 || tile >= n_tiles) return;
 #pragma unroll
-        for (int sidx = 0; sidx < 2; ++sidx) {
-            if (sidx == 1 && nsets == 1) break;
-            const char* base = mixed_v ? (sidx ? set_v1 : set_v0) : (sidx ? set_k1 : set_k0);
-            const char* buf = mixed_v ? ring[4 * sidx + kKRing + tile % kVRing] : ring[4 * sidx + tile % kKRing];
+            for (int sidx = 0; sidx < 2; ++sidx) {
+                if (sidx == 1 && nsets == 1) break;
+                const char* base = mixed_v ? (sidx ? set_v1 : set_v0) : (sidx ? set_k1 : set_k0);
+                const char* buf = mixed_v ? ring[4 * sidx + kKRing + tile % kVRing] : ring[4 * sidx + tile % kKRing];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if (j == 1 && mixed_v) break;
-                const int slab = mixed_v ? wave : (wave - kMixedFull) + 4 * j;
-                const char* slab_base = base + (int64_t)(tile * kKeyTile + 8 * slab) * mixed_stride;
-                lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
+                for (int j = 0; j < 2; ++j) {
+                    if (j == 1 && mixed_v) break;
+                    const int slab = mixed_v ? wave : (wave - kMixedFull) + 4 * j;
+                    const char* slab_base = base + (int64_t)(tile * kKeyTile + 8 * slab) * mixed_stride;
+                    lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
+                }
+            }
+        } else {
+            if (tile >= 0 && tile < n_tiles) {
+#pragma unroll
+                for (int sidx = 0; sidx < 2; ++sidx) {
+                    if (sidx == 1 && (nsets == 1 || mixed_v)) break;
+                    const char* base = mixed_v ? set_v0 : (sidx ? set_k1 : set_k0);
+                    const char* buf = mixed_v ? ring[kKRing + tile % kVRing] : ring[4 * sidx + tile % kKRing];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        if (j == 1 && mixed_v) break;
+                        const int slab = mixed_v ? wave : (wave - kMixedFull) + 4 * j;
+                        const char* slab_base = base + (int64_t)(tile * kKeyTile + 8 * slab) * mixed_stride;
+                        lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
+                    }
+                }
+            }
+            if (!mixed_v && nsets == 2 && vt >= 0 && vt < n_tiles) {
+                const int i = wave - kMixedFull;
+                const uint32_t off_v = ks_bytes == vs_bytes ? mixed_off : lane_off(wave & 1, vs_bytes);
+                char* buf = ring[4 + kKRing + vt % kVRing];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int slab = (i & 1) + 4 * (i >> 1) + 2 * j;
+                    const char* slab_base = set_v1 + (int64_t)(vt * kKeyTile + 8 * slab) * vs_bytes;
+                    lds_dma16(slab_base, off_v, lds_addr(buf + 8 * slab * kRowBytes));
+                }
             }
         }
     };
@@ -923,10 +961,10 @@ __global__ __launch_bounds__(4 * 64, 2) void fused_attention_d64_wide_kernel(Fus
 
 // Mixed workgroups: 12 waves, one workgroup per CU; K and V rings for up to
 // two heads (the key-part merge reuses the first of them).
-template <bool IsBf16>
+template <bool IsBf16, int kKind = kKindMixed>
 __global__ __launch_bounds__(12 * 64, 3) void fused_attention_d64_mixed_kernel(FusedAttentionParams p) {
     __shared__ __attribute__((aligned(16))) char ring[2 * (kKRing + kVRing)][kTileBytes];
-    attention_body<12, IsBf16, false, kKindMixed>(p, ring);
+    attention_body<12, IsBf16, false, kKind>(p, ring);
 }
 
 // ---- short key sequences (k_seq <= 128: the 77-token cross-attention, CLIP).
@@ -1570,8 +1608,16 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
             p.q_blocks = (int32_t)qb32;
             p.mixed_total = (int32_t)total;
             p.mixed_wgs = (int32_t)wgs;
-            if (is_bf16) hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<true>), dim3(p.mixed_wgs), dim3(768), 0, stream, p);
-            else hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<false>), dim3(p.mixed_wgs), dim3(768), 0, stream, p);
+            // workgroups span two heads unless every head holds a whole number of them
+            const bool spans = qb32 % kMixedBlocks != 0 && p.heads * p.batch > 1;
+            const dim3 g(p.mixed_wgs), b(768);
+            if (spans) {
+                if (is_bf16) hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<true, kKindMixed2>), g, b, 0, stream, p);
+                else hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<false, kKindMixed2>), g, b, 0, stream, p);
+            } else {
+                if (is_bf16) hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<true>), g, b, 0, stream, p);
+                else hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<false>), g, b, 0, stream, p);
+            }
             return hipGetLastError();
         }
     }

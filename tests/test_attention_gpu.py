@@ -498,6 +498,24 @@ def test_mixed_workgroups(B, Sq, Sk, H):
     _check_config(B, Sq, Sk, H, seed=960 + H)
 
 
+def test_mixed_workgroups_two_heads_unequal_kv_strides():
+    """Workgroups that stage two heads (128 blocks per head: the second head's V slabs come from the
+    half waves) with K a column slice of a wider buffer (row stride 2W) and V contiguous (stride W),
+    so the two transfer offsets differ."""
+    B, Sq, Sk, H = 2, 4096, 1024, 10
+    W = H * 64
+    qb, kb, vb = seeded(990, B, Sq, W), seeded(991, B, Sk, W), seeded(992, B, Sk, W)
+    kwide = torch.zeros(B, Sk, 2 * W, dtype=torch.float16, device=DEV)
+    kwide[:, :, W:] = to_dev(kb)
+    out = sh.attention(to_dev(qb), kwide[:, :, W:], to_dev(vb), H)
+    torch.cuda.synchronize()
+    got = from_dev(out)
+    for r0, r1 in [(0, 32), (2016, 2080), (4064, 4096)]:
+        ref = oracle.attention_f16_rows(qb, kb, vb, H, r0, r1)
+        assert_parity(got[:, r0:r1], ref[:, r0:r1], label=f"mixed unequal strides rows {r0}:{r1}")
+    assert_parity(got, torch_reference(qb, kb, vb, H), label="mixed unequal strides torch")
+
+
 def test_mixed_workgroups_ragged_rows():
     """T = 2560 with 4090 query rows: rows past Sq in the last block of every head are not stored."""
     B, Sq, Sk, H = 2, 4090, 4096, 10
