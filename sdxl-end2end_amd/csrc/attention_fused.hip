@@ -453,13 +453,12 @@ __device__ __attribute__((always_inline)) inline void attention_body(const Fused
             }
             if (!mixed_v && nsets == 2 && vt >= 0 && vt < n_tiles) {
                 const int i = wave - kMixedFull;
-                const uint32_t off_v = ks_bytes == vs_bytes ? mixed_off : lane_off(wave & 1, vs_bytes);
                 char* buf = ring[4 + kKRing + vt % kVRing];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int slab = (i & 1) + 4 * (i >> 1) + 2 * j;
                     const char* slab_base = set_v1 + (int64_t)(vt * kKeyTile + 8 * slab) * vs_bytes;
-                    lds_dma16(slab_base, off_v, lds_addr(buf + 8 * slab * kRowBytes));
+                    lds_dma16(slab_base, mixed_off, lds_addr(buf + 8 * slab * kRowBytes));
                 }
             }
         }
@@ -1608,8 +1607,10 @@ hipError_t launch_fused_attention_d64(const FusedAttentionParams& params_in, boo
             p.q_blocks = (int32_t)qb32;
             p.mixed_total = (int32_t)total;
             p.mixed_wgs = (int32_t)wgs;
-            // workgroups span two heads unless every head holds a whole number of them
-            const bool spans = qb32 % kMixedBlocks != 0 && p.heads * p.batch > 1;
+            // workgroups span two heads unless every head holds a whole number of
+            // them (the two-head kind takes K and V of one row stride: the half
+            // waves' V transfers reuse their K offsets)
+            const bool spans = qb32 % kMixedBlocks != 0 && p.heads * p.batch > 1 && p.k_row_stride == p.v_row_stride;
             const dim3 g(p.mixed_wgs), b(768);
             if (spans) {
                 if (is_bf16) hipLaunchKernelGGL((fused_attention_d64_mixed_kernel<true, kKindMixed2>), g, b, 0, stream, p);

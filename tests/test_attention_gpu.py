@@ -499,9 +499,10 @@ def test_mixed_workgroups(B, Sq, Sk, H):
 
 
 def test_mixed_workgroups_two_heads_unequal_kv_strides():
-    """Workgroups that stage two heads (128 blocks per head: the second head's V slabs come from the
-    half waves) with K a column slice of a wider buffer (row stride 2W) and V contiguous (stride W),
-    so the two transfer offsets differ."""
+    """Workgroups that stage two heads (128 blocks per head) with K a column slice of a wider buffer
+    (row stride 2W) and V contiguous (stride W): the two transfer offsets differ, so the call runs
+    the mixed kind whose whole waves issue the V slabs (the two-head kind needs equal strides; the
+    configs[2] tests cover it)."""
     B, Sq, Sk, H = 2, 4096, 1024, 10
     W = H * 64
     qb, kb, vb = seeded(990, B, Sq, W), seeded(991, B, Sk, W), seeded(992, B, Sk, W)
